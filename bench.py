@@ -1,0 +1,258 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X SSD forward (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3]
+                    [--state-dtype f32|bf16] [--no-cpu-baseline]
+
+A step is one SSD forward (K1 cumsum -> K2 chunk_state -> K3 state_passing ->
+K4 chunk_scan) over one batch of synthetic inputs already resident in HBM, at
+the Mamba-2-2.7B layer shape by default (C3: batch 4, seqlen 4096, 80 heads,
+head_dim 64, d_state 128, chunk 256, 1 group, bf16 X/B/C, fp32 A, final state
+returned).  Prints ONE JSON line.
+
+Timing follows the reference harness (ShouyangDong/WorkloadSuite
+bench.py:138-170): warmup, then device-synchronised timing of K steps.  Each
+kernel's average launch duration is measured live with HIP events on the
+stream the kernels run on (torch's current stream), and the dominant kernel's
+algorithmic bytes (or flops) per launch over that duration give
+``roofline.achieved``.  ``cpu_baseline`` times the CPU oracle's float32
+restatement of the reference einsum path on a bounded sample (one batch
+element of the same config) on this host's cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+from workloadsuite_amd import ssd as S  # noqa: E402
+from workloadsuite_amd.configs import CONFIGS, HEADLINE, make_inputs  # noqa: E402
+
+METRIC = "SSD fwd tokens/s + MFMA%/HBM% of peak at Mamba-2-2.7B layer, 1 MI355X"
+PEAK_HBM_GBS = 8000.0                      # MI355X HBM3E
+PEAK_TFLOPS = {torch.bfloat16: 2500.0, torch.float16: 2500.0, torch.float32: 157.3}   # dense MFMA
+DTYPE_NAMES = {torch.bfloat16: "bf16", torch.float16: "f16", torch.float32: "f32"}
+
+
+def esize(dt):
+    return torch.tensor([], dtype=dt).element_size()
+
+
+def kernel_model(cfg, state_dtype):
+    """Algorithmic HBM bytes and MFMA flops per launch of each kernel.
+
+    Bytes count every operand read once and every result written once at its
+    storage type (B and C per group, not per head).  Flops count useful work:
+    the causal triangle T_Q = Q(Q+1)/2 of the intra-chunk products.
+    """
+    b, L, h, P, N, Q, g = cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.chunk, cfg.ngroups
+    c = L // Q
+    es, ss = esize(cfg.dtype), esize(state_dtype)
+    x = b * L * h * P * es
+    bc = b * L * g * N * es
+    a = b * L * h * 4
+    acs = b * h * c * Q * 4
+    dec = b * h * c * 4
+    st = b * c * h * P * N * ss
+    fin = b * h * P * N * 4 if cfg.final_state else 0
+    init = b * h * P * N * 4 if cfg.init_state else 0
+    TQ = Q * (Q + 1) // 2
+    return {
+        "chunk_cumsum": dict(bytes=a + acs + dec, flops=b * L * h),
+        "chunk_state": dict(bytes=x + bc + acs + st, flops=2 * b * c * h * Q * P * N),
+        "state_passing": dict(bytes=2 * st + dec + fin + init, flops=2 * b * c * h * P * N),
+        "chunk_scan": dict(bytes=x + 2 * bc + acs + st + x,
+                           flops=b * c * h * (2 * TQ * N + 2 * TQ * P + 2 * Q * N * P)),
+    }
+
+
+def end_to_end_model(cfg):
+    """F_min / B_min per forward: inputs read once, outputs written once; CB per group."""
+    b, L, h, P, N, Q, g = cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.chunk, cfg.ngroups
+    c = L // Q
+    es = esize(cfg.dtype)
+    TQ = Q * (Q + 1) // 2
+    flops = b * c * (g * 2 * TQ * N + h * (2 * TQ * P + 4 * Q * N * P + 2 * N * P))
+    byts = 2 * b * L * h * P * es + 2 * b * L * g * N * es + b * L * h * 4
+    byts += b * h * P * N * 4 * (int(cfg.final_state) + int(cfg.init_state))
+    return flops, byts
+
+
+def time_launches(fn, reps):
+    """Average device time (ms) of fn() over reps back-to-back launches.
+
+    A short device-side sleep is queued first so the host can enqueue all
+    launches before the device reaches the start event: the events then bracket
+    device work only, not host launch latency.
+    """
+    torch.cuda.synchronize()
+    sleep = getattr(torch.cuda, "_sleep", None)
+    if sleep is not None:
+        sleep(20_000_000)
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(reps):
+        fn()
+    end.record()
+    end.synchronize()
+    return start.elapsed_time(end) / reps
+
+
+def cpu_baseline(cfg, budget_s=12.0, max_runs=30):
+    """The oracle's float32 restatement of the reference einsum path (MR:123-162)
+    on one batch element of cfg, on this host's CPU cores."""
+    from oracle import ssd_oracle as O
+
+    sample = cfg.scaled(batch=1)
+    inp = make_inputs(sample, seed=0)
+    torch.set_float32_matmul_precision("highest")
+    args = (inp["X"], inp["A"], inp["B"], inp["C"], sample.chunk)
+    kw = dict(initial_states=inp["init"], dtype=torch.float32)
+    O.ssd_chunked(*args, **kw)  # warmup
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < max_runs):
+        t0 = time.perf_counter()
+        O.ssd_chunked(*args, **kw)
+        times.append(time.perf_counter() - t0)
+    med = statistics.median(times)
+    return {
+        "value": sample.tokens / med,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": (f"{cfg.name} with batch 1 of {cfg.batch} ({sample.tokens} tokens, all {cfg.nheads} heads); "
+                   f"oracle/ssd_oracle.py ssd_chunked in torch float32 on CPU (inputs rounded to "
+                   f"{DTYPE_NAMES[cfg.dtype]} first), median of {len(times)} runs, "
+                   f"{torch.get_num_threads()} intra-op threads, os.cpu_count()={os.cpu_count()}"),
+        "ms_per_forward": med * 1e3,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default=HEADLINE, choices=sorted(CONFIGS))
+    ap.add_argument("--state-dtype", default="f32", choices=["f32", "bf16"])
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--kernel-reps", type=int, default=30)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(the SSD forward shards by batch/head with no communication; see DESIGN.md).",
+              file=sys.stderr)
+        sys.exit(2)
+
+    cfg = CONFIGS[args.config]
+    state_dtype = torch.float32 if args.state_dtype == "f32" else torch.bfloat16
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inp = make_inputs(cfg, seed=0, device=dev)
+    X, A, B, C, init = inp["X"], inp["A"], inp["B"], inp["C"], inp["init"]
+
+    def step():
+        return S.ssd_forward(X, A, B, C, cfg.chunk, initial_states=init,
+                             return_final_states=cfg.final_state, state_dtype=state_dtype)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    ev0.record()
+    for _ in range(args.steps):
+        step()
+    ev1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dev_ms = ev0.elapsed_time(ev1) / args.steps
+    ms_per_step = wall * 1e3 / args.steps
+    tokens_per_s = cfg.tokens * args.steps / wall
+
+    # ---- per-kernel device time, each kernel on its real inputs ----
+    Acs, decay = S.chunk_cumsum(A, cfg.chunk)
+    states = S.chunk_state(X, B, Acs, state_dtype=state_dtype)
+    S_in, _ = S.state_passing(states, decay, init)
+    # K3 is timed in place on its own buffer (re-applying the recurrence to its
+    # output each launch: same traffic, values stay finite at these decays).
+    sp_buf = S_in.clone()
+    sp_final = torch.empty(cfg.batch, cfg.nheads, cfg.headdim, cfg.dstate, device=dev) if cfg.final_state else None
+    kfn = {
+        "chunk_cumsum": lambda: S.chunk_cumsum(A, cfg.chunk),
+        "chunk_state": lambda: S.chunk_state(X, B, Acs, state_dtype=state_dtype),
+        "state_passing": lambda: S.state_passing_(sp_buf, decay, init, sp_final),
+        "chunk_scan": lambda: S.chunk_scan(X, B, C, Acs, S_in),
+    }
+    model = kernel_model(cfg, state_dtype)
+    kernels = {}
+    for name, fn in kfn.items():
+        fn()
+        ms = time_launches(fn, args.kernel_reps)
+        m = model[name]
+        gbs = m["bytes"] / (ms * 1e-3) / 1e9
+        tfs = m["flops"] / (ms * 1e-3) / 1e12
+        t_hbm = m["bytes"] / (PEAK_HBM_GBS * 1e9)
+        t_mfma = m["flops"] / (PEAK_TFLOPS[cfg.dtype] * 1e12)
+        kernels[name] = {
+            "ms": round(ms, 5), "bytes": m["bytes"], "flops": m["flops"],
+            "GB_s": round(gbs, 1), "TFLOP_s": round(tfs, 2),
+            "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "mfma_frac": round(tfs / PEAK_TFLOPS[cfg.dtype], 4),
+            "bound": "hbm" if t_hbm >= t_mfma else "mfma",
+        }
+    dom = max(kernels, key=lambda k: kernels[k]["ms"])
+    kd = kernels[dom]
+    if kd["bound"] == "hbm":
+        roof = {"bound": "hbm", "achieved": kd["GB_s"], "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": kd["hbm_frac"]}
+    else:
+        roof = {"bound": "mfma", "achieved": kd["TFLOP_s"], "peak": PEAK_TFLOPS[cfg.dtype], "unit": "TFLOP/s",
+                "frac": kd["mfma_frac"]}
+    roof["kernel"] = dom
+    roof["traffic"] = None
+
+    f_min, b_min = end_to_end_model(cfg)
+    roof_tps = min(PEAK_TFLOPS[cfg.dtype] * 1e12 / (f_min / cfg.tokens), PEAK_HBM_GBS * 1e9 / (b_min / cfg.tokens))
+
+    out = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": DTYPE_NAMES[cfg.dtype],
+        "data": "synthetic (seeded: X~N(0,1), B,C~N(0,1)/sqrt(N), A=-softplus(N(-2,1))*exp(N(0,.5)))",
+        "config": {"workload": f"mamba2-ssd-forward {cfg.name}" + (" (Mamba-2-2.7B layer)" if cfg.name == "C3" else ""),
+                   "batch": cfg.batch, "seqlen": cfg.seqlen, "nheads": cfg.nheads, "headdim": cfg.headdim,
+                   "dstate": cfg.dstate, "chunk": cfg.chunk, "ngroups": cfg.ngroups,
+                   "inputs": f"{DTYPE_NAMES[cfg.dtype]} X/B/C, f32 A", "state_storage": args.state_dtype,
+                   "final_state": cfg.final_state, "initial_state": cfg.init_state},
+        "device_ms_per_step": round(dev_ms, 5),
+        "roofline": roof,
+        "end_to_end": {"F_min_per_token": f_min / cfg.tokens, "B_min_per_token": b_min / cfg.tokens,
+                       "roofline_tokens_per_s": roof_tps, "frac": round(tokens_per_s / roof_tps, 4)},
+        "kernels": kernels,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(cfg)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

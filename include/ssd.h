@@ -1,0 +1,153 @@
+/*
+ * libssd -- MI355X (gfx950) Mamba-2 SSD forward, C ABI.
+ *
+ * Replaces the hot path of ShouyangDong/WorkloadSuite
+ * workloads/mamba/model_ref.py ("MR"): SSDLayer._ssd_core (MR:123-162), which
+ * its only caller SSDLayer.forward invokes at MR:112.  The reference is pure
+ * Python/PyTorch, so it has no FFI of its own; these entry points are what a
+ * ctypes (or cffi / pybind) binding of that function binds.  The Python side
+ * that mirrors _ssd_core is workloadsuite_amd/ssd.py.
+ *
+ * Conventions
+ *   - Every pointer is a device pointer (HIP device memory) unless noted.
+ *   - Strides are in ELEMENTS; the innermost dimension must have stride 1.
+ *   - `stream` is a hipStream_t (NULL = the default stream).  Every kernel is
+ *     launched on it; nothing synchronises the host.
+ *   - The library allocates nothing, frees nothing and keeps no pointer past
+ *     the call: the caller owns every buffer, workspaces included.
+ *   - Return value: 0 on success, a negative SSD_ERR_* for invalid arguments
+ *     (checked on the host before any launch), a positive hipError_t when a
+ *     launch fails.  ssd_strerror() names both.  No exit/abort in the library.
+ *   - Thread-safe and re-entrant: no global mutable state.
+ *
+ * Layouts (b batch, L seqlen, h heads, P headdim, N dstate, g groups,
+ *          Q chunk, c = L / Q chunks):
+ *   x, y          [b, L, h, P]  dtype (f32 / bf16 / f16)
+ *   a             [b, L, h]     f32   log-decay per token and head, A*dt
+ *   bmat, cmat    [b, L, g, N]  dtype; head i reads group i / (h / g)
+ *   dt            [b, L, h]     f32   optional (NULL means dt == 1)
+ *   a_cumsum      [b, h, c, Q]  f32   contiguous (workspace)
+ *   chunk_decay   [b, h, c]     f32   contiguous (workspace)
+ *   states        [b, c, h, P, N] state dtype, contiguous (workspace)
+ *   initial/final [b, h, P, N]  f32   contiguous, optional
+ */
+#ifndef WORKLOADSUITE_AMD_SSD_H
+#define WORKLOADSUITE_AMD_SSD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SSD_ABI_VERSION 1
+
+/* Element types. */
+enum {
+  SSD_DTYPE_F32 = 0,
+  SSD_DTYPE_BF16 = 1,
+  SSD_DTYPE_F16 = 2,
+};
+
+/* Status codes (negative: rejected on the host before any launch). */
+enum {
+  SSD_OK = 0,
+  SSD_ERR_NULL_POINTER = -1,
+  SSD_ERR_BAD_SHAPE = -2,            /* a dimension is < 1                     */
+  SSD_ERR_SEQLEN_NOT_DIVISIBLE = -3, /* L % Q != 0 (MR:106-110 would raise)    */
+  SSD_ERR_HEADS_NOT_DIVISIBLE = -4,  /* h % g != 0 (MR:37-38 raises)           */
+  SSD_ERR_UNSUPPORTED_DTYPE = -5,
+  SSD_ERR_UNSUPPORTED_HEADDIM = -6,  /* P != 64                                */
+  SSD_ERR_UNSUPPORTED_DSTATE = -7,   /* N not in {16, 32, 64, 128, 256}        */
+  SSD_ERR_UNSUPPORTED_CHUNK = -8,    /* Q not in {64, 128, 256}                */
+  SSD_ERR_BAD_STRIDE = -9,           /* innermost stride != 1, or negative     */
+  SSD_ERR_MISALIGNED = -10,          /* vector-loaded rows not 16-byte aligned */
+  SSD_ERR_WORKSPACE_TOO_SMALL = -11,
+  SSD_ERR_TOO_LARGE = -12,           /* a grid dimension would overflow        */
+};
+
+/* Problem dimensions. */
+typedef struct ssd_dims {
+  int64_t batch;   /* b */
+  int64_t seqlen;  /* L, a multiple of chunk */
+  int64_t nheads;  /* h, a multiple of ngroups */
+  int64_t headdim; /* P */
+  int64_t dstate;  /* N */
+  int64_t ngroups; /* g */
+  int64_t chunk;   /* Q (MR's block_len) */
+} ssd_dims;
+
+/* ABI version of the loaded library (SSD_ABI_VERSION). */
+int ssd_abi_version(void);
+
+/* Static, NUL-terminated description of a status code. */
+const char* ssd_strerror(int status);
+
+/* Host-only validation of dims + dtype; no device call.  Replaces the shape
+ * errors MR raises (MR:37-38 ValueError, MR:106-110 einops error). */
+int ssd_check_dims(const ssd_dims* d, int dtype);
+
+/* Bytes of workspace ssd_forward needs: a_cumsum, chunk_decay and the
+ * per-chunk states (state_dtype: SSD_DTYPE_F32 or SSD_DTYPE_BF16), each
+ * region 256-byte aligned.  0 when dims are invalid. */
+size_t ssd_workspace_bytes(const ssd_dims* d, int state_dtype);
+
+/* K1 -- intra-chunk cumsum of the log-decays and the per-chunk total decay.
+ * Replaces MR:135-136 (torch.cumsum + rearrange) and MR:150 (exp of the last
+ * cumsum).  a_strides: element strides of a over [b, L, h]. */
+int ssd_chunk_cumsum(const ssd_dims* d, const float* a, const int64_t a_strides[3],
+                     float* a_cumsum, float* chunk_decay, void* stream);
+
+/* K2 -- per-chunk local states
+ *   states[b,c,h,p,n] = sum_l x[l,p] dt[l] exp(Acs[Q-1]-Acs[l]) bmat[l,n].
+ * Replaces MR:144 (X*dt) and MR:148-149 (decay_to_end and the 3-operand
+ * einsum).  MR's [.., N, P] state is stored here as [.., P, N]. */
+int ssd_chunk_state(const ssd_dims* d, int dtype,
+                    const void* x, const int64_t x_strides[4],
+                    const void* bmat, const int64_t b_strides[4],
+                    const float* dt, const int64_t dt_strides[3],
+                    const float* a_cumsum, void* states, int state_dtype, void* stream);
+
+/* K3 -- inter-chunk recurrence, in place: on entry states[c] holds chunk c's
+ * local state, on exit the state entering chunk c:
+ *   S_in[0] = initial (or 0), S_in[c+1] = chunk_decay[c] S_in[c] + S_local[c].
+ * Replaces the Python loop at MR:152-157.  final_states (optional) receives
+ * the state after the last chunk, which MR computes and discards (MR:156). */
+int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype,
+                      const float* chunk_decay, const float* initial_states,
+                      float* final_states, void* stream);
+
+/* K4 -- fused chunk scan: writes y once,
+ *   y[l,p] = sum_{s<=l} exp(Acs[l]-Acs[s]) (C_l.B_s) dt[s] x[s,p]
+ *            + exp(Acs[l]) sum_n C[l,n] states[c][p,n].
+ * Replaces MR:139-145 (segsum, mask, C.B^T, Y_diag), MR:160-161 (Y_off) and
+ * MR:162 (the sum). */
+int ssd_chunk_scan(const ssd_dims* d, int dtype,
+                   const void* x, const int64_t x_strides[4],
+                   const void* bmat, const int64_t b_strides[4],
+                   const void* cmat, const int64_t c_strides[4],
+                   const float* dt, const int64_t dt_strides[3],
+                   const float* a_cumsum, const void* states, int state_dtype,
+                   void* y, const int64_t y_strides[4], void* stream);
+
+/* Whole SSD forward (K1..K4 on one stream): the replacement for
+ * SSDLayer._ssd_core (MR:123-162).  workspace must hold
+ * ssd_workspace_bytes(d, state_dtype) bytes, 256-byte aligned. */
+int ssd_forward(const ssd_dims* d, int dtype,
+                const void* x, const int64_t x_strides[4],
+                const float* a, const int64_t a_strides[3],
+                const void* bmat, const int64_t b_strides[4],
+                const void* cmat, const int64_t c_strides[4],
+                const float* dt, const int64_t dt_strides[3],
+                const float* initial_states,
+                void* y, const int64_t y_strides[4],
+                float* final_states,
+                void* workspace, size_t workspace_bytes, int state_dtype,
+                void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WORKLOADSUITE_AMD_SSD_H */

@@ -1,0 +1,138 @@
+"""CPU-only checks of the C ABI: the library loads, exports every symbol
+include/ssd.h declares, and rejects invalid arguments on the host before any
+device call (the failure handling of the path, forced from the host)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+import torch
+
+from workloadsuite_amd import _lib
+from workloadsuite_amd import ssd as S
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "ssd.h")
+
+
+def header_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[a-z_0-9]+\s*\*?\s*(ssd_[a-z_]+)\s*\(", text, flags=re.M)))
+
+
+def test_library_exports_every_header_symbol():
+    lib = _lib.load()
+    declared = header_functions()
+    assert declared == sorted(_lib.EXPORTS)
+    for name in declared:
+        assert hasattr(lib, name), name
+    assert lib.ssd_abi_version() == _lib.SSD_ABI_VERSION
+
+
+def d(**kw):
+    base = dict(batch=2, seqlen=256, nheads=8, headdim=64, dstate=64, ngroups=2, chunk=64)
+    base.update(kw)
+    return _lib.SSDDims(*[base[k] for k in ("batch", "seqlen", "nheads", "headdim", "dstate", "ngroups", "chunk")])
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(), 0),
+    (dict(seqlen=100), -3),
+    (dict(nheads=6, ngroups=4), -4),
+    (dict(headdim=32), -6),
+    (dict(dstate=48), -7),
+    (dict(dstate=256), -7),
+    (dict(chunk=32, seqlen=64), -8),
+    (dict(batch=0), -2),
+    (dict(chunk=0), -2),
+])
+def test_check_dims_codes(kw, code):
+    lib = _lib.load()
+    dims = d(**kw)
+    assert lib.ssd_check_dims(ctypes.byref(dims), _lib.DTYPE_BF16) == code
+
+
+def test_check_dims_dtype_and_null():
+    lib = _lib.load()
+    dims = d()
+    assert lib.ssd_check_dims(ctypes.byref(dims), 7) == -5
+    assert lib.ssd_check_dims(None, 0) == -1
+
+
+def test_strerror_names_every_code():
+    lib = _lib.load()
+    for code in range(-12, 1):
+        msg = lib.ssd_strerror(code).decode()
+        assert msg and "unknown" not in msg
+    assert "unknown" in lib.ssd_strerror(-99).decode()
+
+
+def test_workspace_bytes_layout():
+    lib = _lib.load()
+    dims = d()
+    n32 = lib.ssd_workspace_bytes(ctypes.byref(dims), _lib.DTYPE_F32)
+    n16 = lib.ssd_workspace_bytes(ctypes.byref(dims), _lib.DTYPE_BF16)
+    bhc = 2 * 8 * 4
+    states32 = bhc * 64 * 64 * 4
+    assert n32 >= bhc * 64 * 4 + bhc * 4 + states32 and n32 % 256 == 0
+    assert n32 - n16 == states32 // 2
+    bad = d(seqlen=100)
+    assert lib.ssd_workspace_bytes(ctypes.byref(bad), _lib.DTYPE_F32) == 0
+
+
+def test_entry_points_reject_null_and_bad_strides_before_launch():
+    lib = _lib.load()
+    dims = d()
+    s4 = (ctypes.c_int64 * 4)(256 * 8 * 64, 8 * 64, 64, 1)
+    s3 = (ctypes.c_int64 * 3)(256 * 8, 8, 1)
+    bs4 = (ctypes.c_int64 * 4)(256 * 2 * 64, 2 * 64, 64, 1)
+    fake = ctypes.c_void_p(0x100000)  # never dereferenced: validation fails first
+    # null x
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, None, s4, fake, bs4, None, None, fake, fake, 0, None) == -1
+    # inner stride != 1
+    bad = (ctypes.c_int64 * 4)(256 * 8 * 64, 8 * 64, 1, 8)
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, fake, bad, fake, bs4, None, None, fake, fake, 0, None) == -9
+    # misaligned base pointer
+    mis = ctypes.c_void_p(0x100002)
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, mis, s4, fake, bs4, None, None, fake, fake, 0, None) == -10
+    # row stride not a multiple of 16 bytes
+    odd = (ctypes.c_int64 * 4)(256 * 8 * 64, 8 * 64 + 3, 64, 1)
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, fake, odd, fake, bs4, None, None, fake, fake, 0, None) == -10
+    # bf16 states with f32 inputs are not supported
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 0, fake, s4, fake, bs4, None, None, fake, fake, 1, None) == -5
+    # workspace too small / misaligned
+    assert lib.ssd_forward(ctypes.byref(dims), 1, fake, s4, fake, s3, fake, bs4, fake, bs4, None, None, None,
+                           fake, s4, None, fake, 16, 0, None) == -11
+    assert lib.ssd_forward(ctypes.byref(dims), 1, fake, s4, fake, s3, fake, bs4, fake, bs4, None, None, None,
+                           fake, s4, None, ctypes.c_void_p(0x100010), 1 << 30, 0, None) == -10
+    # state passing: misaligned initial state
+    assert lib.ssd_state_passing(ctypes.byref(dims), fake, 0, fake, ctypes.c_void_p(0x100004), None, None) == -10
+
+
+def test_python_op_refuses_cpu_tensors_instead_of_falling_back():
+    X = torch.zeros(1, 64, 2, 64)
+    A = torch.zeros(1, 64, 2)
+    B = torch.zeros(1, 64, 1, 16)
+    with pytest.raises(ValueError, match="HIP devices only"):
+        S.ssd_forward(X, A, B, B, 64)
+
+
+@pytest.mark.parametrize("kw,msg", [
+    (dict(L=96), "multiple of chunk"),
+    (dict(h=3, g=2), "divisible by n_groups"),
+    (dict(bdtype=torch.float16), "dtype"),
+])
+def test_python_op_shape_errors_mirror_reference(kw, msg):
+    L, h, g = kw.get("L", 128), kw.get("h", 4), kw.get("g", 2)
+    X = torch.zeros(1, L, h, 64)
+    A = torch.zeros(1, L, h)
+    B = torch.zeros(1, L, g, 16, dtype=kw.get("bdtype", torch.float32))
+    with pytest.raises(ValueError, match=msg):
+        S.ssd_forward(X, A, B, B, 64)
+
+
+def test_unsupported_dstate_raises_library_error():
+    with pytest.raises(S.SSDError, match="d_state"):
+        S.workspace_bytes(1, 64, 2, 64, 48, 1, 64)

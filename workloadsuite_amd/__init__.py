@@ -1,0 +1,14 @@
+"""MI355X-native Mamba-2 SSD forward (drop-in for the hot path of
+ShouyangDong/WorkloadSuite ``workloads/mamba/model_ref.py``).
+
+    from workloadsuite_amd import ssd_forward
+    Y = ssd_forward(X, A, B, C, chunk_size=256)
+
+Kernels live in ``libssd.so`` (built by ``python -m workloadsuite_amd.build``);
+the C ABI is ``include/ssd.h``.
+"""
+
+from .ssd import SSDError, chunk_cumsum, chunk_scan, chunk_state, ssd_forward, state_passing, workspace_bytes
+
+__all__ = ["ssd_forward", "chunk_cumsum", "chunk_state", "state_passing", "chunk_scan", "workspace_bytes",
+           "SSDError"]

@@ -1,0 +1,100 @@
+"""ctypes binding of libssd.so (include/ssd.h).
+
+The library is loaded after ``torch`` so that it binds to the HIP runtime
+torch already loaded (both resolve the SONAME libamdhip64.so.7): device
+pointers and streams are then shared with torch's allocator and streams.
+There is no fallback: a missing library raises.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  -- must precede the CDLL, see module docstring
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssd.so")
+
+SSD_ABI_VERSION = 1
+DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
+
+# Every symbol include/ssd.h declares.
+EXPORTS = (
+    "ssd_abi_version",
+    "ssd_strerror",
+    "ssd_check_dims",
+    "ssd_workspace_bytes",
+    "ssd_chunk_cumsum",
+    "ssd_chunk_state",
+    "ssd_state_passing",
+    "ssd_chunk_scan",
+    "ssd_forward",
+)
+
+
+class SSDDims(ctypes.Structure):
+    _fields_ = [(n, ctypes.c_int64) for n in
+                ("batch", "seqlen", "nheads", "headdim", "dstate", "ngroups", "chunk")]
+
+
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_vp = ctypes.c_void_p
+_dims_p = ctypes.POINTER(SSDDims)
+_int = ctypes.c_int
+
+_SIGNATURES = {
+    "ssd_abi_version": (_int, []),
+    "ssd_strerror": (ctypes.c_char_p, [_int]),
+    "ssd_check_dims": (_int, [_dims_p, _int]),
+    "ssd_workspace_bytes": (ctypes.c_size_t, [_dims_p, _int]),
+    "ssd_chunk_cumsum": (_int, [_dims_p, _vp, _i64p, _vp, _vp, _vp]),
+    "ssd_chunk_state": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _int, _vp]),
+    "ssd_state_passing": (_int, [_dims_p, _vp, _int, _vp, _vp, _vp, _vp]),
+    "ssd_chunk_scan": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                              _vp, _vp, _int, _vp, _i64p, _vp]),
+    "ssd_forward": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                           _vp, _vp, _i64p, _vp, _vp, ctypes.c_size_t, _int, _vp]),
+}
+
+_LIB = None
+
+
+class SSDError(RuntimeError):
+    """A nonzero status from libssd (negative: invalid argument; positive: HIP error)."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"libssd status {status}: {message}")
+        self.status = status
+
+
+def load() -> ctypes.CDLL:
+    """Load libssd.so once; raises if it is missing or its ABI does not match."""
+    global _LIB
+    if _LIB is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(
+                f"{LIB_PATH} is missing: build it with `python -m workloadsuite_amd.build` "
+                "(there is no CPU fallback for the SSD forward)")
+        lib = ctypes.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGNATURES.items():
+            fn = getattr(lib, name)
+            fn.restype = res
+            fn.argtypes = args
+        if lib.ssd_abi_version() != SSD_ABI_VERSION:
+            raise RuntimeError(f"libssd ABI {lib.ssd_abi_version()} != expected {SSD_ABI_VERSION}")
+        _LIB = lib
+    return _LIB
+
+
+def check(status: int) -> None:
+    if status != 0:
+        raise SSDError(status, load().ssd_strerror(status).decode())
+
+
+def dims(batch, seqlen, nheads, headdim, dstate, ngroups, chunk) -> SSDDims:
+    return SSDDims(batch, seqlen, nheads, headdim, dstate, ngroups, chunk)
+
+
+def strides(t) -> ctypes.Array:
+    s = t.stride()
+    return (ctypes.c_int64 * len(s))(*s)

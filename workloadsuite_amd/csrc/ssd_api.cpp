@@ -1,0 +1,291 @@
+// C ABI of libssd (declared in include/ssd.h): host-side validation and
+// dispatch to the four kernels.  Nothing here allocates, synchronises or keeps
+// state between calls; every kernel goes to the caller's stream.
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+
+#include "../../include/ssd.h"
+#include "ssd_launch.h"
+
+namespace {
+
+using ssd::ChunkScanArgs;
+using ssd::ChunkStateArgs;
+using ssd::CumsumArgs;
+using ssd::StatePassingArgs;
+
+constexpr size_t kWsAlign = 256;
+
+size_t elem_size(int dtype) { return dtype == SSD_DTYPE_F32 ? 4 : 2; }
+
+bool valid_dtype(int dtype) {
+  return dtype == SSD_DTYPE_F32 || dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16;
+}
+
+// f32 inputs keep f32 states; 16-bit inputs may use f32 or bf16 states.
+bool valid_state_dtype(int dtype, int state_dtype) {
+  if (state_dtype == SSD_DTYPE_F32) return true;
+  return state_dtype == SSD_DTYPE_BF16 && dtype != SSD_DTYPE_F32;
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+int check_dims_impl(const ssd_dims* d, int dtype) {
+  if (!d) return SSD_ERR_NULL_POINTER;
+  if (d->batch < 1 || d->seqlen < 1 || d->nheads < 1 || d->headdim < 1 || d->dstate < 1 ||
+      d->ngroups < 1 || d->chunk < 1)
+    return SSD_ERR_BAD_SHAPE;
+  if (d->seqlen % d->chunk != 0) return SSD_ERR_SEQLEN_NOT_DIVISIBLE;
+  if (d->nheads % d->ngroups != 0) return SSD_ERR_HEADS_NOT_DIVISIBLE;
+  if (!valid_dtype(dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+  if (d->headdim != 64) return SSD_ERR_UNSUPPORTED_HEADDIM;
+  if (d->dstate != 16 && d->dstate != 32 && d->dstate != 64 && d->dstate != 128)
+    return SSD_ERR_UNSUPPORTED_DSTATE;
+  if (d->chunk != 64 && d->chunk != 128 && d->chunk != 256) return SSD_ERR_UNSUPPORTED_CHUNK;
+  const int64_t nchunks = d->seqlen / d->chunk;
+  // Kernels index workgroups and (batch, chunk, head) triples in 32-bit ints.
+  if (d->batch > INT_MAX / nchunks || d->batch * nchunks > INT_MAX / d->nheads) return SSD_ERR_TOO_LARGE;
+  return SSD_OK;
+}
+
+// A strided [.., inner] operand read with 16-byte vector loads.
+int check_vec_operand(const void* p, const int64_t* strides, int n, int dtype) {
+  if (!p || !strides) return SSD_ERR_NULL_POINTER;
+  if (strides[n - 1] != 1) return SSD_ERR_BAD_STRIDE;
+  for (int k = 0; k < n - 1; ++k)
+    if (strides[k] < 0) return SSD_ERR_BAD_STRIDE;
+  if (!aligned16(p)) return SSD_ERR_MISALIGNED;
+  const int64_t es = (int64_t)elem_size(dtype);
+  for (int k = 0; k < n - 1; ++k)
+    if ((strides[k] * es) % 16 != 0) return SSD_ERR_MISALIGNED;
+  return SSD_OK;
+}
+
+// A strided f32 operand read with scalar loads ([b, L, h]).
+int check_scalar_operand(const void* p, const int64_t* strides, int n) {
+  if (!p || !strides) return SSD_ERR_NULL_POINTER;
+  for (int k = 0; k < n; ++k)
+    if (strides[k] < 0) return SSD_ERR_BAD_STRIDE;
+  if ((reinterpret_cast<uintptr_t>(p) & 3u) != 0) return SSD_ERR_MISALIGNED;
+  return SSD_OK;
+}
+
+int hip_status(hipError_t e) { return e == hipSuccess ? SSD_OK : (int)e; }
+
+size_t round_up(size_t v) { return (v + kWsAlign - 1) / kWsAlign * kWsAlign; }
+
+struct WsLayout {
+  size_t acs, decay, states, total;
+};
+
+WsLayout ws_layout(const ssd_dims* d, int state_dtype) {
+  const size_t nchunks = (size_t)(d->seqlen / d->chunk);
+  const size_t bhc = (size_t)d->batch * d->nheads * nchunks;
+  WsLayout w;
+  w.acs = 0;
+  w.decay = round_up(bhc * (size_t)d->chunk * sizeof(float));
+  w.states = w.decay + round_up(bhc * sizeof(float));
+  w.total = w.states + round_up(bhc * (size_t)d->headdim * d->dstate * elem_size(state_dtype));
+  return w;
+}
+
+}  // namespace
+
+extern "C" {
+
+int ssd_abi_version(void) { return SSD_ABI_VERSION; }
+
+const char* ssd_strerror(int status) {
+  switch (status) {
+    case SSD_OK: return "success";
+    case SSD_ERR_NULL_POINTER: return "null pointer argument";
+    case SSD_ERR_BAD_SHAPE: return "every dimension must be >= 1";
+    case SSD_ERR_SEQLEN_NOT_DIVISIBLE: return "seqlen must be a multiple of the chunk size";
+    case SSD_ERR_HEADS_NOT_DIVISIBLE: return "n_heads must be divisible by n_groups";
+    case SSD_ERR_UNSUPPORTED_DTYPE: return "unsupported dtype (f32, bf16, f16; bf16 states need 16-bit inputs)";
+    case SSD_ERR_UNSUPPORTED_HEADDIM: return "unsupported head_dim (must be 64)";
+    case SSD_ERR_UNSUPPORTED_DSTATE: return "unsupported d_state (16, 32, 64 or 128)";
+    case SSD_ERR_UNSUPPORTED_CHUNK: return "unsupported chunk size (64, 128 or 256)";
+    case SSD_ERR_BAD_STRIDE: return "innermost stride must be 1 and strides non-negative";
+    case SSD_ERR_MISALIGNED: return "vector-loaded operands need 16-byte aligned rows and buffers";
+    case SSD_ERR_WORKSPACE_TOO_SMALL: return "workspace too small (see ssd_workspace_bytes)";
+    case SSD_ERR_TOO_LARGE: return "problem too large for 32-bit workgroup indexing";
+    default: break;
+  }
+  if (status > 0) return hipGetErrorString((hipError_t)status);
+  return "unknown ssd status";
+}
+
+int ssd_check_dims(const ssd_dims* d, int dtype) { return check_dims_impl(d, dtype); }
+
+size_t ssd_workspace_bytes(const ssd_dims* d, int state_dtype) {
+  if (check_dims_impl(d, SSD_DTYPE_BF16) != SSD_OK) return 0;
+  if (state_dtype != SSD_DTYPE_F32 && state_dtype != SSD_DTYPE_BF16) return 0;
+  return ws_layout(d, state_dtype).total;
+}
+
+int ssd_chunk_cumsum(const ssd_dims* d, const float* a, const int64_t a_strides[3],
+                     float* a_cumsum, float* chunk_decay, void* stream) {
+  int rc = check_dims_impl(d, SSD_DTYPE_F32);
+  if (rc) return rc;
+  if ((rc = check_scalar_operand(a, a_strides, 3))) return rc;
+  if (!a_cumsum || !chunk_decay) return SSD_ERR_NULL_POINTER;
+  CumsumArgs p;
+  p.a = a;
+  p.sab = a_strides[0];
+  p.sal = a_strides[1];
+  p.sah = a_strides[2];
+  p.acs = a_cumsum;
+  p.decay = chunk_decay;
+  p.batch = (int)d->batch;
+  p.nchunks = (int)(d->seqlen / d->chunk);
+  p.nheads = (int)d->nheads;
+  p.chunk = (int)d->chunk;
+  return hip_status(ssd::launch_chunk_cumsum(p, (hipStream_t)stream));
+}
+
+int ssd_chunk_state(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4],
+                    const void* bmat, const int64_t b_strides[4], const float* dt,
+                    const int64_t dt_strides[3], const float* a_cumsum, void* states,
+                    int state_dtype, void* stream) {
+  int rc = check_dims_impl(d, dtype);
+  if (rc) return rc;
+  if (!valid_state_dtype(dtype, state_dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+  if ((rc = check_vec_operand(x, x_strides, 4, dtype))) return rc;
+  if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
+  if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
+  if (!a_cumsum || !states) return SSD_ERR_NULL_POINTER;
+  if (!aligned16(states)) return SSD_ERR_MISALIGNED;
+  ChunkStateArgs p;
+  p.x = x;
+  p.sxb = x_strides[0];
+  p.sxl = x_strides[1];
+  p.sxh = x_strides[2];
+  p.bm = bmat;
+  p.sbb = b_strides[0];
+  p.sbl = b_strides[1];
+  p.sbg = b_strides[2];
+  p.dt = dt;
+  p.sdb = dt ? dt_strides[0] : 0;
+  p.sdl = dt ? dt_strides[1] : 0;
+  p.sdh = dt ? dt_strides[2] : 0;
+  p.acs = a_cumsum;
+  p.states = states;
+  p.batch = (int)d->batch;
+  p.nchunks = (int)(d->seqlen / d->chunk);
+  p.nheads = (int)d->nheads;
+  p.ngroups = (int)d->ngroups;
+  p.dstate = (int)d->dstate;
+  p.chunk = (int)d->chunk;
+  return hip_status(ssd::launch_chunk_state(p, dtype, state_dtype, (hipStream_t)stream));
+}
+
+int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, const float* chunk_decay,
+                      const float* initial_states, float* final_states, void* stream) {
+  int rc = check_dims_impl(d, SSD_DTYPE_BF16);
+  if (rc) return rc;
+  if (state_dtype != SSD_DTYPE_F32 && state_dtype != SSD_DTYPE_BF16) return SSD_ERR_UNSUPPORTED_DTYPE;
+  if (!states || !chunk_decay) return SSD_ERR_NULL_POINTER;
+  if (!aligned16(states) || (initial_states && !aligned16(initial_states)) ||
+      (final_states && !aligned16(final_states)))
+    return SSD_ERR_MISALIGNED;
+  StatePassingArgs p;
+  p.states = states;
+  p.decay = chunk_decay;
+  p.init = initial_states;
+  p.final_state = final_states;
+  p.batch = (int)d->batch;
+  p.nchunks = (int)(d->seqlen / d->chunk);
+  p.nheads = (int)d->nheads;
+  p.headdim = (int)d->headdim;
+  p.dstate = (int)d->dstate;
+  return hip_status(ssd::launch_state_passing(p, state_dtype, (hipStream_t)stream));
+}
+
+int ssd_chunk_scan(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4],
+                   const void* bmat, const int64_t b_strides[4], const void* cmat,
+                   const int64_t c_strides[4], const float* dt, const int64_t dt_strides[3],
+                   const float* a_cumsum, const void* states, int state_dtype, void* y,
+                   const int64_t y_strides[4], void* stream) {
+  int rc = check_dims_impl(d, dtype);
+  if (rc) return rc;
+  if (!valid_state_dtype(dtype, state_dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+  if ((rc = check_vec_operand(x, x_strides, 4, dtype))) return rc;
+  if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
+  if ((rc = check_vec_operand(cmat, c_strides, 4, dtype))) return rc;
+  if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
+  if (!a_cumsum || !states || !y || !y_strides) return SSD_ERR_NULL_POINTER;
+  if (y_strides[3] != 1 || y_strides[0] < 0 || y_strides[1] < 0 || y_strides[2] < 0) return SSD_ERR_BAD_STRIDE;
+  if ((reinterpret_cast<uintptr_t>(y) & (elem_size(dtype) - 1)) != 0) return SSD_ERR_MISALIGNED;
+  ChunkScanArgs p;
+  p.x = x;
+  p.sxb = x_strides[0];
+  p.sxl = x_strides[1];
+  p.sxh = x_strides[2];
+  p.bm = bmat;
+  p.sbb = b_strides[0];
+  p.sbl = b_strides[1];
+  p.sbg = b_strides[2];
+  p.cm = cmat;
+  p.scb = c_strides[0];
+  p.scl = c_strides[1];
+  p.scg = c_strides[2];
+  p.dt = dt;
+  p.sdb = dt ? dt_strides[0] : 0;
+  p.sdl = dt ? dt_strides[1] : 0;
+  p.sdh = dt ? dt_strides[2] : 0;
+  p.acs = a_cumsum;
+  p.states = states;
+  p.y = y;
+  p.syb = y_strides[0];
+  p.syl = y_strides[1];
+  p.syh = y_strides[2];
+  p.batch = (int)d->batch;
+  p.nchunks = (int)(d->seqlen / d->chunk);
+  p.nheads = (int)d->nheads;
+  p.ngroups = (int)d->ngroups;
+  p.dstate = (int)d->dstate;
+  p.chunk = (int)d->chunk;
+  return hip_status(ssd::launch_chunk_scan(p, dtype, state_dtype, (hipStream_t)stream));
+}
+
+int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4], const float* a,
+                const int64_t a_strides[3], const void* bmat, const int64_t b_strides[4],
+                const void* cmat, const int64_t c_strides[4], const float* dt,
+                const int64_t dt_strides[3], const float* initial_states, void* y,
+                const int64_t y_strides[4], float* final_states, void* workspace,
+                size_t workspace_bytes, int state_dtype, void* stream) {
+  int rc = check_dims_impl(d, dtype);
+  if (rc) return rc;
+  if (!valid_state_dtype(dtype, state_dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+  if (!workspace) return SSD_ERR_NULL_POINTER;
+  if ((reinterpret_cast<uintptr_t>(workspace) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
+  const WsLayout w = ws_layout(d, state_dtype);
+  if (workspace_bytes < w.total) return SSD_ERR_WORKSPACE_TOO_SMALL;
+  // Validate every operand before the first launch, so a bad argument never
+  // leaves a partially computed result behind.
+  if ((rc = check_scalar_operand(a, a_strides, 3))) return rc;
+  if ((rc = check_vec_operand(x, x_strides, 4, dtype))) return rc;
+  if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
+  if ((rc = check_vec_operand(cmat, c_strides, 4, dtype))) return rc;
+  if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
+  if (!y || !y_strides) return SSD_ERR_NULL_POINTER;
+  if ((initial_states && !aligned16(initial_states)) || (final_states && !aligned16(final_states)))
+    return SSD_ERR_MISALIGNED;
+
+  char* ws = static_cast<char*>(workspace);
+  float* acs = reinterpret_cast<float*>(ws + w.acs);
+  float* decay = reinterpret_cast<float*>(ws + w.decay);
+  void* states = ws + w.states;
+  if ((rc = ssd_chunk_cumsum(d, a, a_strides, acs, decay, stream))) return rc;
+  if ((rc = ssd_chunk_state(d, dtype, x, x_strides, bmat, b_strides, dt, dt_strides, acs, states,
+                            state_dtype, stream)))
+    return rc;
+  if ((rc = ssd_state_passing(d, states, state_dtype, decay, initial_states, final_states, stream))) return rc;
+  return ssd_chunk_scan(d, dtype, x, x_strides, bmat, b_strides, cmat, c_strides, dt, dt_strides, acs, states,
+                        state_dtype, y, y_strides, stream);
+}
+
+}  // extern "C"

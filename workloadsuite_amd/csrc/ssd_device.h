@@ -1,0 +1,213 @@
+// Device-side building blocks shared by the SSD kernels (gfx950 / CDNA4).
+//
+// MFMA fragments.  Every matrix product in this library is expressed with the
+// 16x16 MFMA shape and an 8-element-per-lane operand fragment:
+//   lane = 16*g + i  (g = lane group 0..3, i = 0..15)
+//   A operand: lane holds A[row = i][k-slot (g, j)], j = 0..7
+//   B operand: lane holds B[k-slot (g, j)][col = i]
+//   D (f32x4): lane holds D[row = 4*g + jj][col = i], jj = 0..3
+// For bf16/f16 one v_mfma_f32_16x16x32_{bf16,f16} consumes the fragment
+// (k-slot (g, j) is K index 8*g + j); for f32 eight v_mfma_f32_16x16x4_f32
+// consume it, instruction j pairing A and B slot (g, j) across the 4 lane
+// groups.  Which logical index a k-slot stands for is the caller's choice, as
+// long as the A and B fragments agree -- the kernels use that freedom to feed
+// an MFMA result (D layout, 4 consecutive rows per lane) straight back in as
+// an A operand without an LDS round trip.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ssd {
+
+typedef __bf16 bf16;
+typedef _Float16 f16;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kWave = 64;
+constexpr int kXcds = 8;  // MI355X: 8 XCDs, workgroups dispatched round-robin
+
+template <typename T> struct VecT;
+template <> struct VecT<float> { typedef f32x8 v8; typedef f32x4 v4; };
+template <> struct VecT<bf16> { typedef bf16x8 v8; typedef bf16x4 v4; };
+template <> struct VecT<f16> { typedef f16x8 v8; typedef f16x4 v4; };
+template <typename T> using frag8 = typename VecT<T>::v8;
+template <typename T> using vec4 = typename VecT<T>::v4;
+
+// ---------------------------------------------------------------------------
+// MFMA wrappers: D += A * B over one 8-slot fragment.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mma(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma(f16x8 a, f16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mma(f32x8 a, f32x8 b, f32x4 c) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) c = __builtin_amdgcn_mfma_f32_16x16x4f32(a[j], b[j], c, 0, 0, 0);
+  return c;
+}
+
+// ---------------------------------------------------------------------------
+// Conversions (round to nearest even).
+// ---------------------------------------------------------------------------
+template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }
+template <typename T> __device__ __forceinline__ float to_f32(T v) { return (float)v; }
+
+template <typename T> __device__ __forceinline__ frag8<T> zero_frag() {
+  frag8<T> z;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) z[j] = (T)0.0f;
+  return z;
+}
+
+// 16-byte vector loads/stores.  p must be 16-byte aligned.
+template <typename T> __device__ __forceinline__ frag8<T> load8(const T* p);
+template <> __device__ __forceinline__ f32x8 load8<float>(const float* p) {
+  f32x4 lo = *reinterpret_cast<const f32x4*>(p);
+  f32x4 hi = *reinterpret_cast<const f32x4*>(p + 4);
+  f32x8 r;
+  r.lo = lo;
+  r.hi = hi;
+  return r;
+}
+template <> __device__ __forceinline__ bf16x8 load8<bf16>(const bf16* p) {
+  return *reinterpret_cast<const bf16x8*>(p);
+}
+template <> __device__ __forceinline__ f16x8 load8<f16>(const f16* p) {
+  return *reinterpret_cast<const f16x8*>(p);
+}
+
+template <typename T> __device__ __forceinline__ void store8(T* p, frag8<T> v);
+template <> __device__ __forceinline__ void store8<float>(float* p, f32x8 v) {
+  *reinterpret_cast<f32x4*>(p) = v.lo;
+  *reinterpret_cast<f32x4*>(p + 4) = v.hi;
+}
+template <> __device__ __forceinline__ void store8<bf16>(bf16* p, bf16x8 v) {
+  *reinterpret_cast<bf16x8*>(p) = v;
+}
+template <> __device__ __forceinline__ void store8<f16>(f16* p, f16x8 v) {
+  *reinterpret_cast<f16x8*>(p) = v;
+}
+
+// 4-element load (8 bytes for 16-bit types, 16 bytes for f32); p aligned to that.
+template <typename T> __device__ __forceinline__ vec4<T> load4(const T* p) {
+  return *reinterpret_cast<const vec4<T>*>(p);
+}
+template <typename T> __device__ __forceinline__ void store4(T* p, vec4<T> v) {
+  *reinterpret_cast<vec4<T>*>(p) = v;
+}
+
+template <typename T> __device__ __forceinline__ frag8<T> join(vec4<T> lo, vec4<T> hi) {
+  frag8<T> r;
+  r.lo = lo;
+  r.hi = hi;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// Workgroup -> tile mapping.  Hardware dispatches workgroup ids round-robin
+// over the 8 XCDs (id % 8), each with its own L2.  The remap hands every XCD a
+// contiguous range of logical tile ids, so tiles that share operands (the
+// heads of one chunk share B and C when ngroups is small) meet in one L2.
+// Bijective for any nblocks.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int xcd_remap(int bid, int nblocks) {
+  const int per = nblocks / kXcds, rem = nblocks % kXcds;
+  const int x = bid % kXcds, k = bid / kXcds;
+  const int start = x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;
+  return start + k;
+}
+
+// ---------------------------------------------------------------------------
+// Stage a ROWS x COLS tile of a row-major global matrix (unit column stride)
+// into LDS transposed, dst[col * ldp + row], optionally scaling row r by
+// scale[r] (an LDS or global array indexed from the tile's first row).
+// Work unit: 4 rows x (16 / sizeof(T)) columns per thread -- one 16-byte load
+// per row, one 4-element LDS store per column.  Requires ROWS % 4 == 0,
+// COLS % (16 / sizeof(T)) == 0, ldp % 4 == 0 and 16-byte aligned rows.
+// ---------------------------------------------------------------------------
+template <typename T, int ROWS, int COLS, int NTHREADS>
+__device__ __forceinline__ void stage_transposed(const T* __restrict__ src, int64_t row_stride,
+                                                 T* __restrict__ dst, int ldp,
+                                                 const float* scale, int tid) {
+  constexpr int V = 16 / sizeof(T);
+  constexpr int CU = COLS / V;
+  constexpr int UNITS = (ROWS / 4) * CU;
+#pragma unroll
+  for (int u0 = 0; u0 < UNITS; u0 += NTHREADS) {
+    const int u = u0 + tid;
+    if (UNITS % NTHREADS == 0 || u < UNITS) {
+      const int cu = u % CU, r4 = u / CU;
+      const int row = 4 * r4, col = V * cu;
+      float v[4][V];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const T* p = src + (int64_t)(row + rr) * row_stride + col;
+        if constexpr (sizeof(T) == 4) {
+          f32x4 x = *reinterpret_cast<const f32x4*>(p);
+#pragma unroll
+          for (int k = 0; k < V; ++k) v[rr][k] = x[k];
+        } else {
+          frag8<T> x = load8<T>(p);
+#pragma unroll
+          for (int k = 0; k < V; ++k) v[rr][k] = to_f32<T>(x[k]);
+        }
+        if (scale) {
+          const float s = scale[row + rr];
+#pragma unroll
+          for (int k = 0; k < V; ++k) v[rr][k] *= s;
+        }
+      }
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        vec4<T> o;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) o[rr] = from_f32<T>(v[rr][k]);
+        store4<T>(dst + (col + k) * ldp + row, o);
+      }
+    }
+  }
+}
+
+// Stage ROWS x COLS rows unchanged (dst[row * ldp + col]); columns >= ncols_valid
+// are zero-filled (padding of the contraction dimension).
+template <typename T, int ROWS, int COLS, int NTHREADS>
+__device__ __forceinline__ void stage_rows(const T* __restrict__ src, int64_t row_stride,
+                                           T* __restrict__ dst, int ldp, int ncols_valid, int tid) {
+  constexpr int V = 16 / sizeof(T);
+  constexpr int CU = COLS / V;
+  constexpr int UNITS = ROWS * CU;
+#pragma unroll
+  for (int u0 = 0; u0 < UNITS; u0 += NTHREADS) {
+    const int u = u0 + tid;
+    if (UNITS % NTHREADS == 0 || u < UNITS) {
+      const int cu = u % CU, row = u / CU;
+      const int col = V * cu;
+      if (col < ncols_valid) {
+        const T* p = src + (int64_t)row * row_stride + col;
+        if constexpr (sizeof(T) == 4) {
+          *reinterpret_cast<f32x4*>(dst + row * ldp + col) = *reinterpret_cast<const f32x4*>(p);
+        } else {
+          store8<T>(dst + row * ldp + col, load8<T>(p));
+        }
+      } else {
+        if constexpr (sizeof(T) == 4) {
+          *reinterpret_cast<f32x4*>(dst + row * ldp + col) = f32x4{0.f, 0.f, 0.f, 0.f};
+        } else {
+          store8<T>(dst + row * ldp + col, zero_frag<T>());
+        }
+      }
+    }
+  }
+}
+
+}  // namespace ssd

@@ -1,0 +1,62 @@
+// Internal launcher interface between the C ABI (ssd_api.cpp) and the kernel
+// translation units.  Arguments are already validated; launchers only pick a
+// template instantiation, size the grid and launch on `stream`.  They return
+// the hipError_t of the launch.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace ssd {
+
+struct CumsumArgs {
+  const float* a;
+  int64_t sab, sal, sah;  // element strides of a [b, L, h]
+  float* acs;             // [b, h, c, Q]
+  float* decay;           // [b, h, c]
+  int batch, nchunks, nheads, chunk;
+};
+
+struct ChunkStateArgs {
+  const void* x;
+  int64_t sxb, sxl, sxh;  // x [b, L, h, P], unit stride over P
+  const void* bm;
+  int64_t sbb, sbl, sbg;  // bmat [b, L, g, N], unit stride over N
+  const float* dt;        // optional [b, L, h]
+  int64_t sdb, sdl, sdh;
+  const float* acs;       // [b, h, c, Q]
+  void* states;           // [b, c, h, P, N]
+  int batch, nchunks, nheads, ngroups, dstate, chunk;
+};
+
+struct StatePassingArgs {
+  void* states;           // [b, c, h, P, N], in place
+  const float* decay;     // [b, h, c]
+  const float* init;      // optional [b, h, P, N]
+  float* final_state;     // optional [b, h, P, N]
+  int batch, nchunks, nheads, headdim, dstate;
+};
+
+struct ChunkScanArgs {
+  const void* x;
+  int64_t sxb, sxl, sxh;
+  const void* bm;
+  int64_t sbb, sbl, sbg;
+  const void* cm;
+  int64_t scb, scl, scg;
+  const float* dt;
+  int64_t sdb, sdl, sdh;
+  const float* acs;       // [b, h, c, Q]
+  const void* states;     // [b, c, h, P, N] (state entering each chunk)
+  void* y;
+  int64_t syb, syl, syh;  // y [b, L, h, P], unit stride over P
+  int batch, nchunks, nheads, ngroups, dstate, chunk;
+};
+
+// dtype / state_dtype use the SSD_DTYPE_* values of include/ssd.h.
+hipError_t launch_chunk_cumsum(const CumsumArgs& a, hipStream_t stream);
+hipError_t launch_chunk_state(const ChunkStateArgs& a, int dtype, int state_dtype, hipStream_t stream);
+hipError_t launch_state_passing(const StatePassingArgs& a, int state_dtype, hipStream_t stream);
+hipError_t launch_chunk_scan(const ChunkScanArgs& a, int dtype, int state_dtype, hipStream_t stream);
+
+}  // namespace ssd

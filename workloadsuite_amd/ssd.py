@@ -1,0 +1,268 @@
+"""Mamba-2 SSD forward on MI355X -- the host side of ``SSDLayer._ssd_core``.
+
+Reference: ``workloads/mamba/model_ref.py`` (MR) in ShouyangDong/WorkloadSuite,
+``SSDLayer._ssd_core(X_b, B_b, C_b, dt_b, A_dt_b, batch)`` (MR:123-162).  This
+module keeps its argument meaning in unchunked form:
+
+    MR (after MR:97-110)                 here
+    X_b    [b, c, l, h, p]  fp16         X  [b, L, h, P]   f32 / bf16 / f16
+    A_dt_b [b, c, l, h]     fp32         A  [b, L, h]      f32 (the log-decay A*dt)
+    B_b, C_b [b, c, l, h, n] (repeated)  B, C [b, L, g, N] (group i // (h/g), no repeat)
+    dt_b   [b, c, l, h]                  dt [b, L, h] or None (None: X is already scaled)
+    block_len                            chunk_size
+    (zeros, MR:153)                      initial_states [b, h, P, N] or None
+    (discarded, MR:156)                  final state [b, h, P, N] when requested
+    returns Y_diag + Y_off [b,c,l,h,p]   returns Y [b, L, h, P] in X's dtype
+
+and its error behaviour: a seqlen that is not a multiple of the chunk size
+(MR:106-110 raises in einops) and heads not divisible by groups (MR:37-38,
+``ValueError``) raise ``ValueError`` here too.  Like MR, the op is pure: it
+allocates fresh outputs and never mutates its inputs.
+
+All arithmetic runs in libssd.so's four HIP kernels on the tensors' device
+and on torch's current stream.  There is no CPU path: tensors on another
+device, or a missing library, raise.  The op is forward-only (no autograd),
+as the reference harness runs it under ``torch.inference_mode()``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+__all__ = [
+    "ssd_forward",
+    "chunk_cumsum",
+    "chunk_state",
+    "state_passing",
+    "state_passing_",
+    "chunk_scan",
+    "workspace_bytes",
+    "SSDError",
+]
+
+SSDError = _lib.SSDError
+
+_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
+_STATE_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+
+
+def _device_check(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(f"libssd runs on HIP devices only; got a tensor on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _vec_operand(t: torch.Tensor) -> torch.Tensor:
+    """Unit inner stride, 16-byte aligned base and row strides (vector loads)."""
+    es = t.element_size()
+    ok = (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+          and all(s >= 0 and (s * es) % 16 == 0 for s in t.stride()[:-1]))
+    return t if ok else t.clone(memory_format=torch.contiguous_format)
+
+
+def _f32_operand(t):
+    if t is None:
+        return None
+    t = t.detach()
+    if t.dtype != torch.float32:
+        t = t.float()
+    if any(s < 0 for s in t.stride()):
+        t = t.contiguous()
+    return t
+
+
+def _f32_contig(t):
+    if t is None:
+        return None
+    t = t.detach().to(torch.float32)
+    if not t.is_contiguous() or t.data_ptr() % 16:
+        t = t.clone(memory_format=torch.contiguous_format)
+    return t
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev):
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _shape_check(X, A, B, C, chunk_size, dt, initial_states):
+    if X.dim() != 4:
+        raise ValueError(f"X must be [batch, seqlen, nheads, headdim], got {tuple(X.shape)}")
+    b, L, h, P = X.shape
+    if A.shape != (b, L, h):
+        raise ValueError(f"A must be {(b, L, h)}, got {tuple(A.shape)}")
+    if B.dim() != 4 or B.shape[:2] != (b, L) or C.shape != B.shape:
+        raise ValueError(f"B and C must be [batch, seqlen, ngroups, dstate] with batch={b}, seqlen={L}; "
+                         f"got {tuple(B.shape)} and {tuple(C.shape)}")
+    g, N = B.shape[2], B.shape[3]
+    if h % g != 0:
+        raise ValueError("n_heads must be divisible by n_groups")
+    if chunk_size < 1 or L % chunk_size != 0:
+        raise ValueError(f"seqlen {L} is not a multiple of chunk size {chunk_size}")
+    if dt is not None and dt.shape != (b, L, h):
+        raise ValueError(f"dt must be {(b, L, h)}, got {tuple(dt.shape)}")
+    if initial_states is not None and initial_states.shape != (b, h, P, N):
+        raise ValueError(f"initial_states must be {(b, h, P, N)}, got {tuple(initial_states.shape)}")
+    if X.dtype not in _DTYPES:
+        raise ValueError(f"unsupported dtype {X.dtype}")
+    if B.dtype != X.dtype or C.dtype != X.dtype:
+        raise ValueError(f"B and C must have X's dtype {X.dtype}, got {B.dtype} and {C.dtype}")
+    return b, L, h, P, g, N
+
+
+def _dims(b, L, h, P, N, g, Q):
+    d = _lib.dims(b, L, h, P, N, g, Q)
+    rc = _lib.load().ssd_check_dims(ctypes.byref(d), _lib.DTYPE_F32)
+    _lib.check(rc)
+    return d
+
+
+def workspace_bytes(batch, seqlen, nheads, headdim, dstate, ngroups, chunk_size,
+                    state_dtype=torch.float32) -> int:
+    d = _lib.dims(batch, seqlen, nheads, headdim, dstate, ngroups, chunk_size)
+    n = _lib.load().ssd_workspace_bytes(ctypes.byref(d), _STATE_DTYPES[state_dtype])
+    if n == 0:
+        _lib.check(_lib.load().ssd_check_dims(ctypes.byref(d), _lib.DTYPE_F32))
+    return n
+
+
+def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
+                return_final_states=False, state_dtype=torch.float32):
+    """Chunked SSD forward (MR:123-162) on the HIP device.
+
+    Returns Y, or (Y, final_states) with ``return_final_states``.
+    ``state_dtype`` is the storage type of the per-chunk states between the
+    kernels (float32, or bfloat16 for 16-bit inputs); the recurrence itself
+    always runs in float32.
+    """
+    b, L, h, P, g, N = _shape_check(X, A, B, C, chunk_size, dt, initial_states)
+    dev = _device_check(X, A, B, C, dt, initial_states)
+    lib = _lib.load()
+    d = _dims(b, L, h, P, N, g, chunk_size)
+    X = _vec_operand(X.detach())
+    Bm = _vec_operand(B.detach())
+    Cm = _vec_operand(C.detach())
+    A = _f32_operand(A)
+    dt = _f32_operand(dt)
+    init = _f32_contig(initial_states)
+    Y = torch.empty((b, L, h, P), dtype=X.dtype, device=dev)
+    final = torch.empty((b, h, P, N), dtype=torch.float32, device=dev) if return_final_states else None
+    sd = _STATE_DTYPES.get(state_dtype)
+    if sd is None:
+        raise ValueError(f"unsupported state dtype {state_dtype}")
+    ws_n = lib.ssd_workspace_bytes(ctypes.byref(d), sd)
+    ws = torch.empty(ws_n, dtype=torch.uint8, device=dev)
+    rc = lib.ssd_forward(ctypes.byref(d), _DTYPES[X.dtype],
+                         _ptr(X), _lib.strides(X), _ptr(A), _lib.strides(A),
+                         _ptr(Bm), _lib.strides(Bm), _ptr(Cm), _lib.strides(Cm),
+                         _ptr(dt), _lib.strides(dt) if dt is not None else None,
+                         _ptr(init), _ptr(Y), _lib.strides(Y), _ptr(final),
+                         _ptr(ws), ws_n, sd, _stream(dev))
+    _lib.check(rc)
+    return (Y, final) if return_final_states else Y
+
+
+# ---------------------------------------------------------------------------
+# The four kernels one at a time (per-kernel parity tests and timing).
+# ---------------------------------------------------------------------------
+
+def chunk_cumsum(A, chunk_size):
+    """K1: A [b, L, h] -> (Acs [b, h, c, Q], chunk_decay [b, h, c]) (MR:135-136, 150)."""
+    if A.dim() != 3:
+        raise ValueError("A must be [batch, seqlen, nheads]")
+    b, L, h = A.shape
+    dev = _device_check(A)
+    if chunk_size < 1 or L % chunk_size != 0:
+        raise ValueError(f"seqlen {L} is not a multiple of chunk size {chunk_size}")
+    d = _dims(b, L, h, 64, 16, 1, chunk_size)
+    A = _f32_operand(A)
+    nc = L // chunk_size
+    Acs = torch.empty((b, h, nc, chunk_size), dtype=torch.float32, device=dev)
+    decay = torch.empty((b, h, nc), dtype=torch.float32, device=dev)
+    _lib.check(_lib.load().ssd_chunk_cumsum(ctypes.byref(d), _ptr(A), _lib.strides(A), _ptr(Acs),
+                                            _ptr(decay), _stream(dev)))
+    return Acs, decay
+
+
+def chunk_state(X, B, Acs, dt=None, state_dtype=torch.float32):
+    """K2: local states [b, c, h, P, N] (MR:144, 148-149)."""
+    b, L, h, P = X.shape
+    g, N = B.shape[2], B.shape[3]
+    Q = Acs.shape[-1]
+    dev = _device_check(X, B, Acs, dt)
+    d = _dims(b, L, h, P, N, g, Q)
+    X, Bm = _vec_operand(X.detach()), _vec_operand(B.detach())
+    Acs = _f32_contig(Acs)
+    dt = _f32_operand(dt)
+    states = torch.empty((b, L // Q, h, P, N), dtype=state_dtype, device=dev)
+    _lib.check(_lib.load().ssd_chunk_state(
+        ctypes.byref(d), _DTYPES[X.dtype], _ptr(X), _lib.strides(X), _ptr(Bm), _lib.strides(Bm),
+        _ptr(dt), _lib.strides(dt) if dt is not None else None, _ptr(Acs), _ptr(states),
+        _STATE_DTYPES[state_dtype], _stream(dev)))
+    return states
+
+
+def state_passing(states, chunk_decay, initial_states=None, return_final_states=True):
+    """K3: (S_in [b, c, h, P, N], final [b, h, P, N]) from local states (MR:152-157).
+
+    Works on a copy: the input ``states`` is left unchanged.
+    """
+    S = states.detach().clone(memory_format=torch.contiguous_format)
+    final = (torch.empty((S.shape[0], S.shape[2], S.shape[3], S.shape[4]), dtype=torch.float32, device=S.device)
+             if return_final_states else None)
+    state_passing_(S, chunk_decay, initial_states, final)
+    return S, final
+
+
+def state_passing_(states, chunk_decay, initial_states=None, final_states=None):
+    """K3 in place on a contiguous ``states`` buffer (local states in, S_in out);
+    ``final_states`` (optional, [b, h, P, N] float32) receives the last state."""
+    b, nc, h, P, N = states.shape
+    dev = _device_check(states, chunk_decay, initial_states, final_states)
+    if not states.is_contiguous():
+        raise ValueError("state_passing_ needs a contiguous states buffer")
+    d = _dims(b, nc * 64, h, P, N, 1, 64)
+    decay = _f32_contig(chunk_decay)
+    init = _f32_contig(initial_states)
+    if final_states is not None and (final_states.dtype != torch.float32 or not final_states.is_contiguous()
+                                     or final_states.shape != (b, h, P, N)):
+        raise ValueError("final_states must be a contiguous float32 [b, h, P, N] tensor")
+    _lib.check(_lib.load().ssd_state_passing(ctypes.byref(d), _ptr(states), _STATE_DTYPES[states.dtype],
+                                             _ptr(decay), _ptr(init), _ptr(final_states), _stream(dev)))
+    return states
+
+
+def chunk_scan(X, B, C, Acs, states, dt=None):
+    """K4: Y [b, L, h, P] from the states entering each chunk (MR:139-145, 160-162)."""
+    b, L, h, P = X.shape
+    g, N = B.shape[2], B.shape[3]
+    Q = Acs.shape[-1]
+    dev = _device_check(X, B, C, Acs, states, dt)
+    d = _dims(b, L, h, P, N, g, Q)
+    X, Bm, Cm = _vec_operand(X.detach()), _vec_operand(B.detach()), _vec_operand(C.detach())
+    Acs = _f32_contig(Acs)
+    dt = _f32_operand(dt)
+    S = states.detach()
+    if not S.is_contiguous():
+        S = S.contiguous()
+    Y = torch.empty((b, L, h, P), dtype=X.dtype, device=dev)
+    _lib.check(_lib.load().ssd_chunk_scan(
+        ctypes.byref(d), _DTYPES[X.dtype], _ptr(X), _lib.strides(X), _ptr(Bm), _lib.strides(Bm),
+        _ptr(Cm), _lib.strides(Cm), _ptr(dt), _lib.strides(dt) if dt is not None else None,
+        _ptr(Acs), _ptr(S), _STATE_DTYPES[S.dtype], _ptr(Y), _lib.strides(Y), _stream(dev)))
+    return Y
