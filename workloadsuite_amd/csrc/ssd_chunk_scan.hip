@@ -14,7 +14,11 @@
 //   * C fragments of its rows stay in registers for the whole chunk; they are
 //     the A operand of C.S^T and the B operand of (C.B^T)^T.
 //   * Y_off: D[l, p] = C[l, :] . S_in[p, :] from an LDS copy of S_in, then
-//     each row is scaled by exp(Acs[l]).
+//     each row is scaled by exp(Acs[l]).  For 16-bit inputs with f32 states,
+//     S_in is staged as a hi + lo pair of the input type and both parts go
+//     through the MFMA: the state keeps ~16 significant bits instead of the
+//     8 of one bf16 rounding (the state is the largest term of y when the
+//     decay is weak).
 //   * Diagonal, 32 tokens s at a time (LDS-staged B rows and x^T with dt
 //     folded in, shared by the 4 waves): the MFMA computes the transposed
 //     block CB^T[s, l], whose D layout puts 4 consecutive s of one l in each
@@ -44,8 +48,10 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_kernel(ChunkScanArgs p) {
   constexpr int LDS_S = NP + PAD;             // S_in rows [p][n]
   constexpr int LDS_B = NP + PAD;             // B rows [s][n]
   constexpr int LDS_X = kSB + PAD;            // x^T rows [p][s]
+  constexpr bool SPLIT = sizeof(T) == 2 && sizeof(S) == 4;
   __shared__ float acs_l[Q];                  // Acs * log2(e)
   __shared__ __attribute__((aligned(16))) T st_lds[kP * LDS_S];
+  __shared__ __attribute__((aligned(16))) T st_lo_lds[SPLIT ? kP * LDS_S : 8];
   __shared__ __attribute__((aligned(16))) T bs_lds[kSB * LDS_B];
   __shared__ __attribute__((aligned(16))) T xt_lds[kP * LDS_X];
   __shared__ float dt_l[Q];
@@ -74,16 +80,21 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_kernel(ChunkScanArgs p) {
   }
   for (int e = tid; e < kP * (NP / 4); e += 256) {
     const int pp = e / (NP / 4), n4 = 4 * (e % (NP / 4));
-    vec4<T> o;
+    vec4<T> o, lo;
     if (n4 < N) {
       const S* src = sg + pp * N + n4;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = from_f32<T>((float)src[k]);
+      for (int k = 0; k < 4; ++k) {
+        const float v = (float)src[k];
+        o[k] = from_f32<T>(v);
+        lo[k] = from_f32<T>(v - to_f32<T>(o[k]));
+      }
     } else {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) o[k] = (T)0.f;
+      for (int k = 0; k < 4; ++k) o[k] = lo[k] = (T)0.f;
     }
     store4<T>(st_lds + pp * LDS_S + n4, o);
+    if constexpr (SPLIT) store4<T>(st_lo_lds + pp * LDS_S + n4, lo);
   }
 
   // ---- C fragments of this wave's row tiles (rows 16*t + i, t = wave + 4r) ----
@@ -112,6 +123,11 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_kernel(ChunkScanArgs p) {
       const frag8<T> sf = load8<T>(st_lds + (16 * pt + i) * LDS_S + 32 * kc + 8 * g);
 #pragma unroll
       for (int r = 0; r < RT; ++r) acc[r][pt] = mma(cf[r][kc], sf, acc[r][pt]);
+      if constexpr (SPLIT) {
+        const frag8<T> sl = load8<T>(st_lo_lds + (16 * pt + i) * LDS_S + 32 * kc + 8 * g);
+#pragma unroll
+        for (int r = 0; r < RT; ++r) acc[r][pt] = mma(cf[r][kc], sl, acc[r][pt]);
+      }
     }
   }
 #pragma unroll

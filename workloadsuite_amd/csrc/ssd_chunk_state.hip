@@ -14,6 +14,10 @@
 // staged through LDS transposed (x^T with the decay weight folded in,
 // B^T), giving each MFMA lane 8 consecutive tokens per 16-byte LDS read.
 // Output tiles: 4 p-tiles x N/16 n-tiles of 16x16, split over the 4 waves.
+// For 16-bit inputs the decay-weighted x is staged as a bf16/f16 hi + lo pair
+// and both parts go through the MFMA against the exact B: the weighting is
+// then carried to ~2^-16 relative instead of one 2^-9 rounding, at no cost in
+// time because the kernel is bound by HBM, not by the doubled MFMA work.
 // Arithmetic intensity at Q=256, N=128 is ~62 flop/byte (bf16 x in, f32 state
 // out) against a bf16 ridge of ~315: HBM bound.  Workgroup ids are remapped so
 // the heads of one chunk run on one XCD and share the B tile through its L2.
@@ -33,8 +37,10 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(ChunkStateArgs p) {
   constexpr int N = 16 * NT;
   constexpr int PAD = 16 / sizeof(T);
   constexpr int LDP = kLB + PAD;
+  constexpr bool SPLIT = sizeof(T) == 2;
   __shared__ float w_l[256];
   __shared__ __attribute__((aligned(16))) T xt[kP * LDP];
+  __shared__ __attribute__((aligned(16))) T xt_lo[SPLIT ? kP * LDP : 8];
   __shared__ __attribute__((aligned(16))) T bt[N * LDP];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
@@ -71,7 +77,10 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(ChunkStateArgs p) {
 
   for (int lb = 0; lb < Q; lb += kLB) {
     __syncthreads();
-    stage_transposed<T, kLB, kP, 256>(xg + lb * p.sxl, p.sxl, xt, LDP, w_l + lb, tid);
+    if constexpr (SPLIT)
+      stage_transposed_split<T, kLB, kP, 256>(xg + lb * p.sxl, p.sxl, xt, xt_lo, LDP, w_l + lb, tid);
+    else
+      stage_transposed<T, kLB, kP, 256>(xg + lb * p.sxl, p.sxl, xt, LDP, w_l + lb, tid);
     stage_transposed<T, kLB, N, 256>(bg + lb * p.sbl, p.sbl, bt, LDP, nullptr, tid);
     __syncthreads();
 #pragma unroll
@@ -85,6 +94,14 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(ChunkStateArgs p) {
       for (int a = 0; a < PTW; ++a)
 #pragma unroll
         for (int n = 0; n < NTW; ++n) acc[a][n] = mma(af[a], bf[n], acc[a][n]);
+      if constexpr (SPLIT) {
+#pragma unroll
+        for (int a = 0; a < PTW; ++a) af[a] = load8<T>(xt_lo + (16 * (pt0 + a) + i) * LDP + 32 * ks + 8 * g);
+#pragma unroll
+        for (int a = 0; a < PTW; ++a)
+#pragma unroll
+          for (int n = 0; n < NTW; ++n) acc[a][n] = mma(af[a], bf[n], acc[a][n]);
+      }
     }
   }
 

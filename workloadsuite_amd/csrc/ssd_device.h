@@ -178,6 +178,48 @@ __device__ __forceinline__ void stage_transposed(const T* __restrict__ src, int6
   }
 }
 
+// As stage_transposed, for 16-bit T, writing the scaled value v as two
+// T-valued parts: hi = round(v) to dst_hi and lo = round(v - hi) to dst_lo.
+// hi + lo carries ~16 significant bits, so an MFMA pair (hi, lo) against an
+// exact 16-bit operand reproduces the f32-scaled product to ~2^-16 relative
+// instead of the 2^-9 of a single rounding.
+template <typename T, int ROWS, int COLS, int NTHREADS>
+__device__ __forceinline__ void stage_transposed_split(const T* __restrict__ src, int64_t row_stride,
+                                                       T* __restrict__ dst_hi, T* __restrict__ dst_lo,
+                                                       int ldp, const float* scale, int tid) {
+  static_assert(sizeof(T) == 2, "split staging is for 16-bit element types");
+  constexpr int V = 8;
+  constexpr int CU = COLS / V;
+  constexpr int UNITS = (ROWS / 4) * CU;
+#pragma unroll
+  for (int u0 = 0; u0 < UNITS; u0 += NTHREADS) {
+    const int u = u0 + tid;
+    if (UNITS % NTHREADS == 0 || u < UNITS) {
+      const int cu = u % CU, r4 = u / CU;
+      const int row = 4 * r4, col = V * cu;
+      float v[4][V];
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const frag8<T> x = load8<T>(src + (int64_t)(row + rr) * row_stride + col);
+        const float s = scale ? scale[row + rr] : 1.f;
+#pragma unroll
+        for (int k = 0; k < V; ++k) v[rr][k] = to_f32<T>(x[k]) * s;
+      }
+#pragma unroll
+      for (int k = 0; k < V; ++k) {
+        vec4<T> hi, lo;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          hi[rr] = from_f32<T>(v[rr][k]);
+          lo[rr] = from_f32<T>(v[rr][k] - to_f32<T>(hi[rr]));
+        }
+        store4<T>(dst_hi + (col + k) * ldp + row, hi);
+        store4<T>(dst_lo + (col + k) * ldp + row, lo);
+      }
+    }
+  }
+}
+
 // Stage ROWS x COLS rows unchanged (dst[row * ldp + col]); columns >= ncols_valid
 // are zero-filled (padding of the contraction dimension).
 template <typename T, int ROWS, int COLS, int NTHREADS>
