@@ -27,6 +27,7 @@ SOURCES = [
     "ssd_chunk_state.hip",
     "ssd_state_passing.hip",
     "ssd_chunk_scan.hip",
+    "ssd_chunk_scan_q256.hip",
 ]
 
 # Packed FP32 VALU forms are disabled: hipcc -O3 would otherwise emit

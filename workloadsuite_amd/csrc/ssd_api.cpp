@@ -3,6 +3,7 @@
 // state between calls; every kernel goes to the caller's stream.
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cstdint>
 
@@ -72,6 +73,20 @@ int check_scalar_operand(const void* p, const int64_t* strides, int n) {
   return SSD_OK;
 }
 
+// The output y [b, L, h, P] is written 4 elements at a time: unit inner
+// stride, non-negative strides, 4-element aligned base and row strides.
+int check_output(const void* y, const int64_t* strides, int dtype) {
+  if (!y || !strides) return SSD_ERR_NULL_POINTER;
+  if (strides[3] != 1) return SSD_ERR_BAD_STRIDE;
+  const int64_t es = (int64_t)elem_size(dtype), align = 4 * es;
+  for (int k = 0; k < 3; ++k) {
+    if (strides[k] < 0) return SSD_ERR_BAD_STRIDE;
+    if ((strides[k] * es) % align != 0) return SSD_ERR_MISALIGNED;
+  }
+  if ((int64_t)(reinterpret_cast<uintptr_t>(y) % (uintptr_t)align) != 0) return SSD_ERR_MISALIGNED;
+  return SSD_OK;
+}
+
 int hip_status(hipError_t e) { return e == hipSuccess ? SSD_OK : (int)e; }
 
 size_t round_up(size_t v) { return (v + kWsAlign - 1) / kWsAlign * kWsAlign; }
@@ -92,6 +107,25 @@ WsLayout ws_layout(const ssd_dims* d, int state_dtype) {
 }
 
 }  // namespace
+
+namespace ssd {
+
+int device_cu_count() {
+  constexpr int kMaxDevices = 64;
+  static std::atomic<int> cache[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < kMaxDevices) {
+    const int n = cache[dev].load(std::memory_order_relaxed);
+    if (n > 0) return n;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < kMaxDevices) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+}  // namespace ssd
 
 extern "C" {
 
@@ -216,9 +250,8 @@ int ssd_chunk_scan(const ssd_dims* d, int dtype, const void* x, const int64_t x_
   if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
   if ((rc = check_vec_operand(cmat, c_strides, 4, dtype))) return rc;
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
-  if (!a_cumsum || !states || !y || !y_strides) return SSD_ERR_NULL_POINTER;
-  if (y_strides[3] != 1 || y_strides[0] < 0 || y_strides[1] < 0 || y_strides[2] < 0) return SSD_ERR_BAD_STRIDE;
-  if ((reinterpret_cast<uintptr_t>(y) & (elem_size(dtype) - 1)) != 0) return SSD_ERR_MISALIGNED;
+  if (!a_cumsum || !states) return SSD_ERR_NULL_POINTER;
+  if ((rc = check_output(y, y_strides, dtype))) return rc;
   ChunkScanArgs p;
   p.x = x;
   p.sxb = x_strides[0];
@@ -271,7 +304,7 @@ int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_str
   if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
   if ((rc = check_vec_operand(cmat, c_strides, 4, dtype))) return rc;
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
-  if (!y || !y_strides) return SSD_ERR_NULL_POINTER;
+  if ((rc = check_output(y, y_strides, dtype))) return rc;
   if ((initial_states && !aligned16(initial_states)) || (final_states && !aligned16(final_states)))
     return SSD_ERR_MISALIGNED;
 

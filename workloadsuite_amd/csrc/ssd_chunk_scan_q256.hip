@@ -1,0 +1,432 @@
+// K4 -- chunk_scan, persistent variant for 16-bit inputs at chunk 256 (the
+// Mamba-2-2.7B layer shape).  Same result as the generic kernel in
+// ssd_chunk_scan.hip (workloads/mamba/model_ref.py:139-145, 160-162):
+//   y[l, p] = sum_{s<=l} exp(Acs[l]-Acs[s]) (C_l . B_s) dt[s] x[s, p]
+//             + exp(Acs[l]) sum_n C[l, n] S_in[p, n]
+//
+// Work decomposition.  One workgroup of 8 waves per CU loops over a
+// contiguous range of (b, c, h) items, heads fastest, so consecutive items
+// share (b, c) and usually the group of B and C.
+//   * C . B^T depends on (b, c, group) only.  Wave w owns row tiles w and
+//     15-w (16 rows each; every wave then has 17 causal 16x16 blocks in 9
+//     32-token s blocks) and keeps their CB^T blocks in registers as f32 MFMA
+//     D fragments, recomputed only when the group changes (B and C are read
+//     from global memory then; they are shared by all heads of the group and
+//     sit in L2).
+//   * Per item two products remain, computed transposed, D = Y^T[p, l], so
+//     each lane ends with 4 consecutive p of one row (8-byte y stores):
+//       off-diagonal  Y^T = exp(Acs[l]) S_in[p, :] . C[l, :]
+//       diagonal      Y^T += x^T[p, s] (exp(Acs[l]-Acs[s]) dt[s] CB^T[s, l])
+//     The weighted CB^T block is a D fragment with 4 consecutive s of one l
+//     per lane, i.e. already the B operand of the diagonal MFMA.  Below the
+//     diagonal the decay factors around the last token r of each 32-token s
+//     block, exp(Acs[l]-Acs[r]) exp(Acs[r]-Acs[s]) (both <= 1 for decaying
+//     A): one exp per lane and block plus a per-item table of the second
+//     factor, instead of one exp per element.  The block that crosses the
+//     diagonal keeps the exact per-element form, masked before its exponent
+//     can overflow.
+//   * x^T operands come straight from row-major x in LDS through the
+//     transposing read ds_read_b64_tr_b16.  S_in (f32) is split once per item,
+//     in LDS, into a bf16 hi + lo pair that both go through the MFMA, so the
+//     state keeps ~16 significant bits.
+// Data movement.  The next item's x, S_in, Acs and dt are copied global ->
+// LDS by global_load_lds (no VGPRs held) into the second of two LDS buffers
+// while the current item computes; one wait + barrier per item publishes
+// them.  x rows are XOR-swizzled by 16-byte piece at copy time (the copy
+// picks each lane's global address) and S_in rows are copied one per
+// instruction with 16 bytes of padding between rows, so the transposing reads
+// of x and the row reads of S_in are free of bank conflicts.  Every operand
+// read uses a per-lane base computed once plus a compile-time offset.  y
+// stores of an item are issued at the start of the next one so their latency
+// overlaps its compute.
+//
+// Traffic per item: x 32 KB + S_in 32 KB (f32) + Acs 1 KB read, y 32 KB
+// written; B and C per group from L2.  HBM bound at this shape.
+#include <type_traits>
+
+#include "ssd_device.h"
+#include "ssd_launch.h"
+#include "../../include/ssd.h"
+
+namespace ssd {
+
+namespace {
+
+constexpr int kP = 64;
+constexpr int kQ = 256;
+constexpr int kNT = kQ / 16;         // row tiles
+constexpr int kNW = kNT / 2;         // waves: wave w owns row tiles w and kNT-1-w
+constexpr int kThreads = 64 * kNW;
+constexpr int kNPair = kNT / 2 + 1;  // 32-token s blocks per wave, both tiles
+constexpr int kXBlocks = kQ / 8;     // 1 KB copy blocks of x (8 rows of 64 x 16-bit)
+
+struct Item {
+  int b, c, h, grp;
+};
+
+__device__ __forceinline__ Item item_of(const ChunkScanArgs& p, int it) {
+  Item r;
+  r.h = it % p.nheads;
+  const int bc = it / p.nheads;
+  r.c = bc % p.nchunks;
+  r.b = bc / p.nchunks;
+  r.grp = r.h / (p.nheads / p.ngroups);
+  return r;
+}
+
+template <typename T, typename S, int NK, bool HAS_DT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void chunk_scan_q256_kernel(ChunkScanArgs p) {
+  constexpr int N = 32 * NK;                      // dstate (64 or 128)
+  constexpr bool SPLIT = sizeof(S) == 4;          // f32 states become a hi/lo pair
+  constexpr int LPR = N * (int)sizeof(S) / 16;    // 16-byte pieces per S_in row
+  constexpr int ROWB = N * (int)sizeof(S) + 16;   // S_in row stride in LDS (padded 16 B)
+  // Two buffers of each: the current item's and the next item's (in flight).
+  __shared__ __attribute__((aligned(1024))) T xr[2][kQ * kP];
+  __shared__ __attribute__((aligned(16))) unsigned char sr[2][kP * ROWB];
+  __shared__ __attribute__((aligned(16))) float ar[2][kQ];
+  // G[s] = exp(Acs[r] - Acs[s]), r the last token of s's 32-token block
+  // (written by convert(); the decay of the blocks below the diagonal factors
+  // as exp(Acs[l] - Acs[r]) * G[s]).
+  __shared__ __attribute__((aligned(16))) float gr[2][kQ];
+  __shared__ __attribute__((aligned(16))) float dr[HAS_DT ? 2 : 1][HAS_DT ? kQ : 4];
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __builtin_assume(wave < kNW);  // lets the tile-range tests below fold
+  const int g = lane >> 4, i = lane & 15;
+  const int nitems = p.batch * p.nchunks * p.nheads;
+  const int it0 = (int)((int64_t)blockIdx.x * nitems / gridDim.x);
+  const int it1 = (int)((int64_t)(blockIdx.x + 1) * nitems / gridDim.x);
+  if (it0 >= it1) return;
+  const int ta = wave, tb = kNT - 1 - wave;
+  const int KA = ta / 2 + 1;  // s blocks of tile ta; tile tb has the other kNPair - KA
+
+  // ---- per-lane LDS offsets of the MFMA operands (fixed for the kernel) ----
+  int xoff[4];  // x^T operand: rows 4g + i/4 (+ 32 sb + 16 h), columns 16 pt + 4 (i % 4), swizzled
+  int soff[4];  // S_in operand: row 16 pt + i, states 8 g .. 8 g + 7 of each 32-state K step (bytes)
+  {
+    const int r = 4 * g + (i >> 2), x7 = r & 7;
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+      xoff[pt] = r * kP + 8 * ((2 * pt + ((i & 3) >> 1)) ^ x7) + 4 * (i & 1);
+      soff[pt] = (16 * pt + i) * ROWB + g * (SPLIT ? 32 : 16);
+    }
+  }
+
+
+  // ---- per-lane parts of the copy and store addresses (fixed for the kernel) ----
+  // x copy: lane reads row (lane / 8) of its 8-row block, piece (lane % 8) ^ (lane / 8).
+  const int64_t xcopy = (int64_t)(lane >> 3) * p.sxl + 8 * ((lane & 7) ^ (lane >> 3));
+  // y store: row 16 t + i, columns 16 pt + 4 g .. + 3 of each tile t.
+  const int64_t yrow0 = (int64_t)(16 * ta + i) * p.syl + 4 * g;
+  const int64_t yrow1 = (int64_t)(16 * tb + i) * p.syl + 4 * g;
+
+  // ---- global -> LDS copy of one item's x, S_in, Acs (and dt) into buffer b ----
+  auto issue_copy = [&](int it, int b) __attribute__((always_inline)) {
+    const Item r = item_of(p, it);
+    const int64_t l0 = (int64_t)r.c * kQ;
+    const T* xg = reinterpret_cast<const T*>(p.x) + r.b * p.sxb + l0 * p.sxl + r.h * p.sxh + xcopy;
+    // x: copy block blk holds rows 8 blk .. 8 blk + 7; row s keeps piece c at slot c ^ (s & 7).
+#pragma unroll
+    for (int m = 0; m < kXBlocks / kNW; ++m) {
+      const int blk = wave + kNW * m;
+      dma16(xg + (int64_t)(8 * blk) * p.sxl, xr[b] + blk * 512);
+    }
+    // S_in: one row per copy (LPR lanes), rows ROWB bytes apart.
+    const S* sg = reinterpret_cast<const S*>(p.states) +
+                  (((int64_t)r.b * p.nchunks + r.c) * p.nheads + r.h) * (int64_t)(kP * N) +
+                  lane * (16 / (int)sizeof(S));
+#pragma unroll
+    for (int m = 0; m < kP / kNW; ++m) {
+      const int row = wave + kNW * m;
+      const uint32_t dst = lds_offset(sr[b] + row * ROWB);
+      if (lane < LPR) dma16_at(sg + row * N, dst);
+    }
+    if (wave == kNW - 1) {
+      const float* ag = p.acs + (((int64_t)r.b * p.nheads + r.h) * p.nchunks + r.c) * kQ;
+      dma16(ag + 4 * lane, ar[b]);
+    }
+    if constexpr (HAS_DT) {
+      if (wave < kQ / 64) {
+        const float* dg = p.dt + r.b * p.sdb + r.h * p.sdh;
+        dma4(dg + (l0 + 64 * wave + lane) * p.sdl, dr[b] + 64 * wave);
+      }
+    }
+  };
+
+  // ---- once the copy of buffer b has landed: Acs *= log2(e); S_in -> MFMA operand type ----
+  // f32 S_in: each 32-byte pair of pieces (8 states) becomes [hi x8 | lo x8] of T in place.
+  // bf16 S_in with f16 inputs: converted to f16 in place.
+  auto convert = [&](int b) __attribute__((always_inline)) {
+    for (int e = tid; e < kQ; e += kThreads) {
+      const float a = ar[b][e] * kLog2e, ar_end = ar[b][e | 31] * kLog2e;
+      gr[b][e] = __builtin_amdgcn_exp2f(ar_end - a);
+    }
+    __syncthreads();  // every G read its block's unscaled last Acs
+    for (int e = tid; e < kQ; e += kThreads) ar[b][e] *= kLog2e;
+    if constexpr (SPLIT) {
+      for (int u = tid; u < kP * (N / 8); u += kThreads) {
+        const int row = u / (N / 8), q = u % (N / 8);
+        unsigned char* pr = sr[b] + row * ROWB + 32 * q;
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(pr);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(pr + 16);
+        frag8<T> hi, lo;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          hi[k] = from_f32<T>(v0[k]);
+          lo[k] = from_f32<T>(v0[k] - to_f32<T>(hi[k]));
+          hi[4 + k] = from_f32<T>(v1[k]);
+          lo[4 + k] = from_f32<T>(v1[k] - to_f32<T>(hi[4 + k]));
+        }
+        *reinterpret_cast<frag8<T>*>(pr) = hi;
+        *reinterpret_cast<frag8<T>*>(pr + 16) = lo;
+      }
+    } else if constexpr (!std::is_same<S, T>::value) {
+      for (int u = tid; u < kP * LPR; u += kThreads) {
+        unsigned char* pr = sr[b] + (u / LPR) * ROWB + 16 * (u % LPR);
+        const frag8<S> v = *reinterpret_cast<const frag8<S>*>(pr);
+        frag8<T> o;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) o[k] = from_f32<T>(to_f32<S>(v[k]));
+        *reinterpret_cast<frag8<T>*>(pr) = o;
+      }
+    }
+  };
+
+  // ---- per-group registers: C fragments of both tiles and their CB^T blocks ----
+  frag8<T> cf[2][NK];
+  f32x4 cbc[kNPair][2];
+  auto load_group = [&](int it) __attribute__((always_inline)) {
+    int lane_o = lane;
+    asm volatile("" : "+v"(lane_o));
+    const int g = lane_o >> 4, i = lane_o & 15;
+    const Item r = item_of(p, it);
+    const int64_t l0 = (int64_t)r.c * kQ;
+    const T* cg = reinterpret_cast<const T*>(p.cm) + r.b * p.scb + l0 * p.scl + r.grp * p.scg;
+    const T* bg = reinterpret_cast<const T*>(p.bm) + r.b * p.sbb + l0 * p.sbl + r.grp * p.sbg;
+#pragma unroll
+    for (int kc = 0; kc < NK; ++kc) {
+      cf[0][kc] = load8<T>(cg + (int64_t)(16 * ta + i) * p.scl + 32 * kc + 8 * g);
+      cf[1][kc] = load8<T>(cg + (int64_t)(16 * tb + i) * p.scl + 32 * kc + 8 * g);
+    }
+    // One 32-token s block (two 16x16 sub-tiles) per step; every row lies in
+    // the chunk, so all loads of a step issue together, and a sub-tile
+    // entirely above the diagonal is zeroed after its MFMAs.
+#pragma unroll
+    for (int k = 0; k < kNPair; ++k) {
+      // cbc[k]: tile ta's s block k for k < KA, else tile tb's s block kNPair-1-k
+      // (reverse order, so step j of either tile sits at a compile-time index)
+      const bool first = k < KA;
+      const int t = first ? ta : tb, sb = first ? k : kNPair - 1 - k;
+      frag8<T> bfr[2][NK], cfx[NK];
+#pragma unroll
+      for (int kc = 0; kc < NK; ++kc) {
+        cfx[kc] = first ? cf[0][kc] : cf[1][kc];
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+          bfr[st][kc] = load8<T>(bg + (int64_t)(32 * sb + 16 * st + i) * p.sbl + 32 * kc + 8 * g);
+      }
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kc = 0; kc < NK; ++kc) d = mma(bfr[st][kc], cfx[kc], d);
+        const bool live = 2 * sb + st <= t;
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) cbc[k][st][jj] = live ? d[jj] : 0.f;
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // ---- one item from LDS buffer b into packed y registers ----
+  // Both row tiles together: the off-diagonal reads each S_in fragment once
+  // for both, and diagonal step j of the two tiles shares one 32-token s
+  // block, so its x^T fragments and G factors are read once and feed two
+  // independent MFMA chains.
+  vec4<T> ypk[2][4];
+  auto compute = [&](int b) __attribute__((always_inline)) {
+    const T* xb = xr[b];
+    const unsigned char* sbuf = sr[b];
+    const float* ab = ar[b];
+    const float* gb = gr[b];
+    const float* db = dr[HAS_DT ? b : 0];
+    const int KB = kNPair - KA;
+    float al[2];
+    al[0] = ab[16 * ta + i];  // Acs[l] * log2(e) of this lane's row in each tile
+    al[1] = ab[16 * tb + i];
+    f32x4 acc[2][4];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) acc[s2][pt] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // off-diagonal: acc[s2][pt] = S_in[p, :] . C[l, :], then * exp(Acs[l])
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+#pragma unroll
+      for (int kc = 0; kc < NK; ++kc) {
+        const unsigned char* q = sbuf + soff[pt] + kc * (SPLIT ? 128 : 64);
+        const frag8<T> hi = *reinterpret_cast<const frag8<T>*>(q);
+        acc[0][pt] = mma(hi, cf[0][kc], acc[0][pt]);
+        acc[1][pt] = mma(hi, cf[1][kc], acc[1][pt]);
+        if constexpr (SPLIT) {
+          const frag8<T> lo = *reinterpret_cast<const frag8<T>*>(q + 16);
+          acc[0][pt] = mma(lo, cf[0][kc], acc[0][pt]);
+          acc[1][pt] = mma(lo, cf[1][kc], acc[1][pt]);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);  // bound how far LDS reads are hoisted (register pressure)
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      const float e = __builtin_amdgcn_exp2f(al[s2]);
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) acc[s2][pt] *= e;
+    }
+
+    // weighted CB^T block of one tile and s block as an MFMA operand; only
+    // the block that crosses the diagonal needs the causal mask.
+    auto weights = [&](int s2, int sb, const f32x4* cb, bool on_diag, const f32x4* gs) __attribute__((always_inline)) {
+      frag8<T> af;
+      const int l = 16 * (s2 ? tb : ta) + i;
+      if (on_diag) {
+        // exact decay, masked before it can overflow above the diagonal
+#pragma unroll
+        for (int st = 0; st < 2; ++st) {
+          const f32x4 as = *reinterpret_cast<const f32x4*>(ab + 32 * sb + 16 * st + 4 * g);
+          f32x4 ds = f32x4{1.f, 1.f, 1.f, 1.f};
+          if constexpr (HAS_DT) ds = *reinterpret_cast<const f32x4*>(db + 32 * sb + 16 * st + 4 * g);
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) {
+            float w = __builtin_amdgcn_exp2f(al[s2] - as[jj]) * cb[st][jj];
+            if constexpr (HAS_DT) w *= ds[jj];
+            af[4 * st + jj] = from_f32<T>((32 * sb + 16 * st + 4 * g + jj <= l) ? w : 0.f);
+          }
+        }
+      } else {
+        // below the diagonal: exp(Acs[l] - Acs[s]) = exp(Acs[l] - Acs[r]) G[s]
+        const float fl = __builtin_amdgcn_exp2f(al[s2] - ab[32 * sb + 31]);
+#pragma unroll
+        for (int st = 0; st < 2; ++st)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) af[4 * st + jj] = from_f32<T>(cb[st][jj] * (fl * gs[st][jj]));
+      }
+      return af;
+    };
+
+    // diagonal, step j: s block j of tile ta (j < KA) and of tile tb (j < KB)
+#pragma unroll
+    for (int j = 0; j < kNPair - 1; ++j) {
+      const bool do_a = j < KA, do_b = j < KB;  // wave-uniform
+      if (!do_b) continue;                       // KB >= KA: nothing left for either tile
+      f32x4 gs[2];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        gs[st] = *reinterpret_cast<const f32x4*>(gb + 32 * j + 16 * st + 4 * g);
+        if constexpr (HAS_DT) gs[st] *= *reinterpret_cast<const f32x4*>(db + 32 * j + 16 * st + 4 * g);
+      }
+      frag8<T> xfr[4];
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) {
+        const T* a0 = xb + xoff[pt] + (32 * j) * kP;
+        xfr[pt] = join<T>(lds_read_tr(a0), lds_read_tr(a0 + 16 * kP));
+      }
+      {
+        const frag8<T> af = weights(1, j, cbc[kNPair - 1 - j], j == KB - 1, gs);
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) acc[1][pt] = mma(xfr[pt], af, acc[1][pt]);
+      }
+      if (do_a) {
+        const frag8<T> af = weights(0, j, cbc[j], j == KA - 1, gs);
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) acc[0][pt] = mma(xfr[pt], af, acc[0][pt]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) ypk[s2][pt][jj] = from_f32<T>(acc[s2][pt][jj]);
+  };
+
+  auto store_y = [&](const Item& r) __attribute__((always_inline)) {
+    T* yg = reinterpret_cast<T*>(p.y) + r.b * p.syb + ((int64_t)r.c * kQ) * p.syl + r.h * p.syh;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; ++s2) {
+      T* yrow = yg + (s2 ? yrow1 : yrow0);
+#pragma unroll
+      for (int pt = 0; pt < 4; ++pt) store4<T>(yrow + 16 * pt, ypk[s2][pt]);
+    }
+  };
+
+  // Per item: start the next item's copy, store the previous item's y,
+  // compute this one; then wait for the copy, publish it, convert it, and
+  // publish the conversion.
+  Item cur = item_of(p, it0), prev = cur;
+  issue_copy(it0, 0);
+  load_group(it0);
+  dma_wait();
+  __syncthreads();
+  convert(0);
+  __syncthreads();
+  for (int it = it0; it < it1; ++it) {
+    const int bc = (it - it0) & 1, bn = bc ^ 1;
+    const bool has_next = it + 1 < it1;
+    if (has_next) issue_copy(it + 1, bn);
+    if (it > it0) store_y(prev);
+    compute(bc);
+    dma_wait();
+    __syncthreads();
+    prev = cur;
+    if (has_next) {
+      convert(bn);
+      const Item nxt = item_of(p, it + 1);
+      if (nxt.b != cur.b || nxt.c != cur.c || nxt.grp != cur.grp) load_group(it + 1);
+      cur = nxt;
+    }
+    __syncthreads();
+  }
+  store_y(prev);
+}
+
+template <typename T, typename S, int NK>
+hipError_t launch_nk(const ChunkScanArgs& a, hipStream_t stream) {
+  auto kern = a.dt ? chunk_scan_q256_kernel<T, S, NK, true> : chunk_scan_q256_kernel<T, S, NK, false>;
+  const int items = a.batch * a.nchunks * a.nheads;
+  const int grid = persistent_grid(kern, kThreads, items);
+  kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+template <typename T, typename S>
+hipError_t launch_ts(const ChunkScanArgs& a, hipStream_t stream) {
+  switch (a.dstate) {
+    case 64: return launch_nk<T, S, 2>(a, stream);
+    case 128: return launch_nk<T, S, 4>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool chunk_scan_persistent_supported(const ChunkScanArgs& a, int dtype) {
+  // dstate 16 / 32 stay on the generic kernel (this one spills registers there).
+  return a.chunk == kQ && (a.dstate == 64 || a.dstate == 128) &&
+         (dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16);
+}
+
+hipError_t launch_chunk_scan_persistent(const ChunkScanArgs& a, int dtype, int state_dtype, hipStream_t stream) {
+  if (state_dtype == SSD_DTYPE_F32) {
+    if (dtype == SSD_DTYPE_BF16) return launch_ts<bf16, float>(a, stream);
+    if (dtype == SSD_DTYPE_F16) return launch_ts<f16, float>(a, stream);
+  } else if (state_dtype == SSD_DTYPE_BF16) {
+    if (dtype == SSD_DTYPE_BF16) return launch_ts<bf16, bf16>(a, stream);
+    if (dtype == SSD_DTYPE_F16) return launch_ts<f16, bf16>(a, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ssd

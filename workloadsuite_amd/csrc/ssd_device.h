@@ -69,6 +69,15 @@ template <typename T> __device__ __forceinline__ frag8<T> zero_frag() {
   return z;
 }
 
+// v if keep, else zeros (a per-lane select, no branch).
+template <typename T> __device__ __forceinline__ frag8<T> select_frag(bool keep, frag8<T> v) {
+  typedef uint32_t u32v __attribute__((ext_vector_type(sizeof(frag8<T>) / 4)));
+  u32v w = __builtin_bit_cast(u32v, v);
+#pragma unroll
+  for (int j = 0; j < (int)(sizeof(frag8<T>) / 4); ++j) w[j] = keep ? w[j] : 0u;
+  return __builtin_bit_cast(frag8<T>, w);
+}
+
 // 16-byte vector loads/stores.  p must be 16-byte aligned.
 template <typename T> __device__ __forceinline__ frag8<T> load8(const T* p);
 template <> __device__ __forceinline__ f32x8 load8<float>(const float* p) {
@@ -112,6 +121,74 @@ template <typename T> __device__ __forceinline__ frag8<T> join(vec4<T> lo, vec4<
   r.hi = hi;
   return r;
 }
+
+// ---------------------------------------------------------------------------
+// gfx950 LDS transfer primitives.
+// ---------------------------------------------------------------------------
+template <typename V> using lds_ptr = __attribute__((address_space(3))) V*;
+
+// Transposing 8-byte LDS read (ds_read_b64_tr_b16).  Within each group of 16
+// lanes, lane j returns element (j % 4) of the 8-byte chunks addressed by
+// lanes 4r + j/4 of its group, r = 0..3.  So if lane k of a group addresses
+// the 4 consecutive columns c0 + 4(k%4) .. +3 of row r0 + k/4 of a row-major
+// 16-bit matrix, lane j receives column c0 + j of rows r0 .. r0+3: a 4 x 16
+// block read transposed, as an MFMA operand wants it.
+__device__ __forceinline__ bf16x4 lds_read_tr(const bf16* p) {
+  return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_ptr<bf16x4>)(const_cast<bf16*>(p)));
+}
+__device__ __forceinline__ f16x4 lds_read_tr(const f16* p) {
+  typedef __fp16 fp16x4_builtin __attribute__((ext_vector_type(4)));  // the builtin's element type
+  const fp16x4_builtin r =
+      __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_ptr<fp16x4_builtin>)(const_cast<f16*>(p)));
+  return __builtin_bit_cast(f16x4, r);
+}
+
+// Asynchronous global -> LDS copy (global_load_lds_dwordx4 / _dword): lane k
+// reads 16 (or 4) bytes at its own global address g and the hardware writes
+// them to lds_base + 16k (or + 4k); lds_base is taken from the first lane
+// (it must be wave-uniform).  The copy is counted by vmcnt: wait with
+// dma_wait() before the barrier that publishes the data.
+//
+// Issued through inline asm (M0 saved and restored around it) rather than
+// __builtin_amdgcn_global_load_lds: the compiler then does not track the
+// copy, and so cannot place conservative vmcnt(0) waits before unrelated LDS
+// reads of the other buffer -- which would serialise the copy of the next
+// work item with the compute of the current one.  The price is that the
+// caller owns the wait.  Callers must not have compiler-issued global loads
+// in flight alongside an outstanding copy (their partial vmcnt waits would
+// not count it).
+__device__ __forceinline__ uint32_t lds_offset(const void* lds) {
+  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr<const void>)lds);
+}
+// As dma16, with the LDS destination already a wave-uniform LDS offset (from
+// lds_offset(), computed outside any lane-divergent branch the copy sits in).
+__device__ __forceinline__ void dma16_at(const void* g, uint32_t lds_off) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(lds_off)
+      : "memory");
+}
+__device__ __forceinline__ void dma16(const void* g, void* lds_base) { dma16_at(g, lds_offset(lds_base)); }
+__device__ __forceinline__ void dma4(const void* g, void* lds_base) {
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(lds_offset(lds_base))
+      : "memory");
+}
+// s_waitcnt vmcnt(0): every vector memory operation of this wave has completed.
+__device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
 // ---------------------------------------------------------------------------
 // Workgroup -> tile mapping.  Hardware dispatches workgroup ids round-robin

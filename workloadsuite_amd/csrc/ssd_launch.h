@@ -53,10 +53,34 @@ struct ChunkScanArgs {
   int batch, nchunks, nheads, ngroups, dstate, chunk;
 };
 
+// Compute units of the current device (cached per device id after the first
+// query; 0 when the query fails).
+int device_cu_count();
+
+// Workgroups for a persistent kernel that loops over `items` work items:
+// every workgroup slot the kernel's occupancy allows on the device's CUs,
+// capped by the item count.  `kernel` is the __global__ function.
+template <typename K>
+int persistent_grid(K kernel, int threads, int items) {
+  int per_cu = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, reinterpret_cast<const void*>(kernel), threads, 0) !=
+          hipSuccess ||
+      per_cu < 1)
+    per_cu = 1;
+  const int cus = device_cu_count();
+  const long slots = (long)(cus > 0 ? cus : 256) * per_cu;
+  return (int)(slots < items ? slots : items);
+}
+
 // dtype / state_dtype use the SSD_DTYPE_* values of include/ssd.h.
 hipError_t launch_chunk_cumsum(const CumsumArgs& a, hipStream_t stream);
 hipError_t launch_chunk_state(const ChunkStateArgs& a, int dtype, int state_dtype, hipStream_t stream);
 hipError_t launch_state_passing(const StatePassingArgs& a, int state_dtype, hipStream_t stream);
 hipError_t launch_chunk_scan(const ChunkScanArgs& a, int dtype, int state_dtype, hipStream_t stream);
+
+// chunk_scan's persistent kernel for 16-bit inputs at chunk 256
+// (ssd_chunk_scan_q256.hip); launch_chunk_scan dispatches to it when supported.
+bool chunk_scan_persistent_supported(const ChunkScanArgs& a, int dtype);
+hipError_t launch_chunk_scan_persistent(const ChunkScanArgs& a, int dtype, int state_dtype, hipStream_t stream);
 
 }  // namespace ssd
