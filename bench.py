@@ -87,6 +87,19 @@ def end_to_end_model(cfg):
     return flops, byts
 
 
+def profiled_traffic(cfg, kernel):
+    """HBM bytes per launch of `kernel` as measured with rocprofv3 FETCH_SIZE /
+    WRITE_SIZE (scaled by a copy of known size) and committed under profiles/;
+    (None, None) when there is no such measurement for this workload."""
+    path = os.path.join(ROOT, "profiles", f"ssd_forward_{cfg.name}.md")
+    if kernel != "chunk_scan" or not os.path.exists(path):
+        return None, None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(line.split(":")[1]), os.path.relpath(path, ROOT)
+    return None, None
+
+
 def time_launches(fn, reps):
     """Average device time (ms) of fn() over reps back-to-back launches.
 
@@ -147,13 +160,26 @@ def main():
     ap.add_argument("--state-dtype", default="f32", choices=["f32", "bf16"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=30)
+    ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
+                    help="only run a plain device-to-device copy of MB MiB (5 times) and exit: the "
+                         "reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print("bench.py measures one GPU only: this build has no multi-GPU path "
-              "(the SSD forward shards by batch/head with no communication; see DESIGN.md).",
-              file=sys.stderr)
+        print("bench.py measures one GPU only: this build has no multi-GPU path. The SSD forward "
+              "shards over batch x heads with no communication, so N GPUs would each run this "
+              "single-GPU workload on 1/N of the heads.", file=sys.stderr)
         sys.exit(2)
+
+    if args.copy_probe:
+        n = args.copy_probe << 20
+        src = torch.ones(n, dtype=torch.uint8, device="cuda:0")
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes": n, "launches": 5}), flush=True)
+        return
 
     cfg = CONFIGS[args.config]
     state_dtype = torch.float32 if args.state_dtype == "f32" else torch.bfloat16
@@ -220,7 +246,7 @@ def main():
         roof = {"bound": "mfma", "achieved": kd["TFLOP_s"], "peak": PEAK_TFLOPS[cfg.dtype], "unit": "TFLOP/s",
                 "frac": kd["mfma_frac"]}
     roof["kernel"] = dom
-    roof["traffic"] = None
+    roof["traffic"], roof["traffic_source"] = profiled_traffic(cfg, dom)
 
     f_min, b_min = end_to_end_model(cfg)
     roof_tps = min(PEAK_TFLOPS[cfg.dtype] * 1e12 / (f_min / cfg.tokens), PEAK_HBM_GBS * 1e9 / (b_min / cfg.tokens))

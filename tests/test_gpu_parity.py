@@ -319,3 +319,26 @@ def test_model_surface(name):
                           initial_states=inputs[1][:1].cpu() if len(inputs) > 1 else None)
     atol = 1e-4 * Yr.abs().max().item() if name == "C1" else 1e-4
     assert_close(Y[:1], Yr, 1e-4, atol=atol)
+
+
+def test_ssd_core_takes_the_reference_arguments():
+    """MR:123-162's own argument layout: chunked [b, c, l, ...] tensors, B/C
+    repeated per head, X unscaled with dt separate, f16 data (the reference's
+    dtype) -- against the sequential scan."""
+    say("ssd_core reference layout")
+    b, c, l, h, p, n, g = 2, 3, 64, 8, 64, 32, 2
+    gen = torch.Generator().manual_seed(11)
+    x = torch.randn(b, c * l, h, p, generator=gen).half()
+    Bg = (torch.randn(b, c * l, g, n, generator=gen) / math.sqrt(n)).half()
+    Cg = (torch.randn(b, c * l, g, n, generator=gen) / math.sqrt(n)).half()
+    dt = torch.nn.functional.softplus(torch.randn(b, c * l, h, generator=gen) - 1.0)
+    A = -torch.rand(h, generator=gen) - 0.5
+    A_dt = A * dt
+    Brep = Bg.repeat_interleave(h // g, dim=2)
+    Crep = Cg.repeat_interleave(h // g, dim=2)
+    chunk = lambda t: t.reshape(b, c, l, *t.shape[2:])  # noqa: E731
+    Y = S.ssd_core(chunk(x).to(DEV), chunk(Brep).to(DEV), chunk(Crep).to(DEV), chunk(dt).to(DEV),
+                   chunk(A_dt).to(DEV), b)
+    assert Y.shape == (b, c, l, h, p) and Y.dtype == torch.float16
+    Ys, _ = O.ssd_sequential(x, A_dt, Bg, Cg, dt=dt)
+    assert_close(Y.reshape(b, c * l, h, p), Ys, 2e-2)

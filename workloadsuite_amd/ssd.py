@@ -35,6 +35,7 @@ from . import _lib
 
 __all__ = [
     "ssd_forward",
+    "ssd_core",
     "chunk_cumsum",
     "chunk_state",
     "state_passing",
@@ -175,6 +176,22 @@ def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
                          _ptr(ws), ws_n, sd, _stream(dev))
     _lib.check(rc)
     return (Y, final) if return_final_states else Y
+
+
+def ssd_core(X_b, B_b, C_b, dt_b, A_dt_b, batch=None, state_dtype=torch.float32):
+    """``SSDLayer._ssd_core`` (MR:123-162) with the reference's own arguments.
+
+    X_b [b, c, l, h, p]; B_b, C_b [b, c, l, h, n] (already GQA-repeated,
+    MR:97-99); dt_b, A_dt_b [b, c, l, h]; ``batch`` is accepted and ignored
+    (MR passes it to size its zero initial state).  Returns Y [b, c, l, h, p]
+    in X_b's dtype, like MR:162.  The block length is l (MR's block_len).
+    """
+    b, c, l, h, p = X_b.shape
+    L = c * l
+    Y = ssd_forward(X_b.reshape(b, L, h, p), A_dt_b.reshape(b, L, h),
+                    B_b.reshape(b, L, h, B_b.shape[-1]), C_b.reshape(b, L, h, C_b.shape[-1]),
+                    chunk_size=l, dt=dt_b.reshape(b, L, h), state_dtype=state_dtype)
+    return Y.reshape(b, c, l, h, p)
 
 
 # ---------------------------------------------------------------------------
