@@ -25,6 +25,7 @@ SOURCES = [
     "ssd_api.cpp",
     "ssd_cumsum.hip",
     "ssd_chunk_state.hip",
+    "ssd_chunk_state_q256.hip",
     "ssd_state_passing.hip",
     "ssd_chunk_scan.hip",
     "ssd_chunk_scan_q256.hip",

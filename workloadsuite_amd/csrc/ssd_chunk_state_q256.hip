@@ -1,0 +1,252 @@
+// K2 -- chunk_state, persistent variant for 16-bit inputs at chunk 256 (the
+// Mamba-2-2.7B layer shape).  Same result as the generic kernel in
+// ssd_chunk_state.hip (workloads/mamba/model_ref.py:144, 148-149):
+//   S[p, n] = sum_l x[l, p] dt[l] exp(Acs[Q-1] - Acs[l]) B[l, n]
+// stored as states[b, c, h, p, n].
+//
+// Work decomposition.  Workgroups of 8 waves loop over contiguous ranges of
+// (b, c, h) items, heads fastest, so a workgroup's items share (b, c) and
+// usually the group of B.  The product is computed transposed,
+//   S^T[n, p] = sum_l (B^T[n, l] w[l]) x[l, p],   w[l] = exp(Acs[Q-1]-Acs[l]) dt[l],
+// so that each lane ends with 4 consecutive n of one p (16-byte stores).
+//   * B is per group: wave w owns one 16-wide n tile and keeps its B^T
+//     fragments for the whole chunk in registers, loaded only when the group
+//     changes.  Per item the weight w[l] is applied to them in registers and
+//     the product is split into a hi + lo pair of the input type, so the
+//     weighting keeps ~16 significant bits through the MFMA.
+//   * x comes straight from row-major x in LDS through the transposing read
+//     ds_read_b64_tr_b16 (x^T is never staged).
+// Data movement.  The next item's x, Acs (and dt) are copied global -> LDS by
+// global_load_lds into the second of two LDS buffers while the current item
+// computes; x rows are XOR-swizzled by 16-byte piece at copy time so the
+// transposing reads are free of bank conflicts.  After the copy lands the
+// weights w[l] are tabulated in LDS once per item.  States are stored at the
+// start of the next item so the store latency overlaps its compute.
+//
+// Traffic per item: x 32 KB + Acs 1 KB read, states 32 KB (f32) written; B
+// once per group.  HBM bound at this shape.
+#include "ssd_device.h"
+#include "ssd_launch.h"
+#include "../../include/ssd.h"
+
+namespace ssd {
+
+namespace {
+
+constexpr int kP = 64;
+constexpr int kQ = 256;
+constexpr int kNW = 8;               // waves per workgroup
+constexpr int kThreads = 64 * kNW;
+constexpr int kKS = kQ / 32;         // 32-token K steps
+constexpr int kXBlocks = kQ / 8;     // 1 KB copy blocks of x (8 rows of 64 x 16-bit)
+
+struct Item {
+  int b, c, h, grp;
+};
+
+__device__ __forceinline__ Item item_of(const ChunkStateArgs& p, int it) {
+  Item r;
+  r.h = it % p.nheads;
+  const int bc = it / p.nheads;
+  r.c = bc % p.nchunks;
+  r.b = bc / p.nchunks;
+  r.grp = r.h / (p.nheads / p.ngroups);
+  return r;
+}
+
+template <typename S> struct StateStore;
+template <> struct StateStore<float> {
+  __device__ static void store(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
+};
+template <> struct StateStore<bf16> {
+  __device__ static void store(bf16* p, f32x4 v) {
+    bf16x4 o = {(bf16)v[0], (bf16)v[1], (bf16)v[2], (bf16)v[3]};
+    *reinterpret_cast<bf16x4*>(p) = o;
+  }
+};
+
+// K slot j of lane group g stands for token 4 g + j (j < 4) or 16 + 4 g + j - 4
+// (j >= 4) of a 32-token step: the rows a pair of transposing reads delivers.
+__device__ __forceinline__ int slot_token(int g, int j) { return (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4)); }
+
+template <typename T, typename S, int NK, bool HAS_DT>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
+void chunk_state_q256_kernel(ChunkStateArgs p) {
+  constexpr int N = 32 * NK;        // dstate (64 or 128)
+  constexpr int NTILE = N / 16;     // n tiles
+  constexpr int PTW = NTILE / 2;    // p tiles per wave (4 for N=128, 2 for N=64)
+  __shared__ __attribute__((aligned(1024))) T xr[2][kQ * kP];
+  __shared__ __attribute__((aligned(16))) float ar[2][kQ];
+  __shared__ __attribute__((aligned(16))) float dr[HAS_DT ? 2 : 1][HAS_DT ? kQ : 4];
+  __shared__ __attribute__((aligned(16))) float wr[kQ];  // w[l] of the current item
+
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  __builtin_assume(wave < kNW);
+  const int g = lane >> 4, i = lane & 15;
+  const int nitems = p.batch * p.nchunks * p.nheads;
+  const int it0 = (int)((int64_t)blockIdx.x * nitems / gridDim.x);
+  const int it1 = (int)((int64_t)(blockIdx.x + 1) * nitems / gridDim.x);
+  if (it0 >= it1) return;
+  const int nt = wave % NTILE, pt0 = (wave / NTILE) * PTW;  // this wave's n tile and first p tile
+
+  // ---- per-lane offsets (fixed for the kernel) ----
+  // x operand via transposing reads: rows 4 g + i/4 (+ 16, + 32 ks), columns 16 pt + 4 (i % 4), swizzled.
+  int xoff[PTW];
+  {
+    const int r = 4 * g + (i >> 2), x7 = r & 7;
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) {
+      const int pt = pt0 + q;
+      xoff[q] = r * kP + 8 * ((2 * pt + ((i & 3) >> 1)) ^ x7) + 4 * (i & 1);
+    }
+  }
+  const int64_t xcopy = (int64_t)(lane >> 3) * p.sxl + 8 * ((lane & 7) ^ (lane >> 3));
+  // states [p][n]: row 16 pt + i, columns 16 nt + 4 g .. + 3
+  const int srow = (16 * pt0 + i) * N + 16 * nt + 4 * g;
+
+  auto issue_copy = [&](int it, int b) __attribute__((always_inline)) {
+    const Item r = item_of(p, it);
+    const int64_t l0 = (int64_t)r.c * kQ;
+    const T* xg = reinterpret_cast<const T*>(p.x) + r.b * p.sxb + l0 * p.sxl + r.h * p.sxh + xcopy;
+#pragma unroll
+    for (int m = 0; m < kXBlocks / kNW; ++m) {
+      const int blk = wave + kNW * m;
+      dma16(xg + (int64_t)(8 * blk) * p.sxl, xr[b] + blk * 512);
+    }
+    if (wave == kNW - 1) {
+      const float* ag = p.acs + (((int64_t)r.b * p.nheads + r.h) * p.nchunks + r.c) * kQ;
+      dma16(ag + 4 * lane, ar[b]);
+    }
+    if constexpr (HAS_DT) {
+      if (wave < kQ / 64) {
+        const float* dg = p.dt + r.b * p.sdb + r.h * p.sdh;
+        dma4(dg + (l0 + 64 * wave + lane) * p.sdl, dr[b] + 64 * wave);
+      }
+    }
+  };
+
+  // w[l] = exp(Acs[Q-1] - Acs[l]) dt[l] of the item in buffer b
+  auto tabulate = [&](int b) __attribute__((always_inline)) {
+    for (int l = tid; l < kQ; l += kThreads) {
+      float w = __builtin_amdgcn_exp2f((ar[b][kQ - 1] - ar[b][l]) * kLog2e);
+      if constexpr (HAS_DT) w *= dr[b][l];
+      wr[l] = w;
+    }
+  };
+
+  // ---- per-group registers: B^T fragments of this wave's n tile, one per K step ----
+  frag8<T> bt[kKS];
+  auto load_group = [&](int it) __attribute__((always_inline)) {
+    int lane_o = lane;
+    asm volatile("" : "+v"(lane_o));  // opaque: per-group address math, not hoisted
+    const int go = lane_o >> 4, io = lane_o & 15;
+    const Item r = item_of(p, it);
+    const int64_t l0 = (int64_t)r.c * kQ;
+    const T* bg = reinterpret_cast<const T*>(p.bm) + r.b * p.sbb + l0 * p.sbl + r.grp * p.sbg + 16 * nt + io;
+#pragma unroll
+    for (int ks = 0; ks < kKS; ++ks)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) bt[ks][j] = bg[(int64_t)(32 * ks + slot_token(go, j)) * p.sbl];
+  };
+
+  // ---- one item from LDS buffer b into the state registers ----
+  f32x4 acc[PTW];
+  auto compute = [&](int b) __attribute__((always_inline)) {
+    const T* xb = xr[b];
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < kKS; ++ks) {
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 4 * g);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 16 + 4 * g);
+      frag8<T> hi, lo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = to_f32<T>(bt[ks][j]) * (j < 4 ? w0[j] : w1[j - 4]);
+        hi[j] = from_f32<T>(v);
+        lo[j] = from_f32<T>(v - to_f32<T>(hi[j]));
+      }
+#pragma unroll
+      for (int q = 0; q < PTW; ++q) {
+        const T* a0 = xb + xoff[q] + (32 * ks) * kP;
+        const frag8<T> xfr = join<T>(lds_read_tr(a0), lds_read_tr(a0 + 16 * kP));
+        acc[q] = mma(hi, xfr, acc[q]);
+        acc[q] = mma(lo, xfr, acc[q]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  f32x4 st_prev[PTW];
+  auto store_states = [&](const Item& r) __attribute__((always_inline)) {
+    S* sg = reinterpret_cast<S*>(p.states) + (((int64_t)r.b * p.nchunks + r.c) * p.nheads + r.h) * (int64_t)(kP * N);
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) StateStore<S>::store(sg + srow + 16 * N * q, st_prev[q]);
+  };
+
+  Item cur = item_of(p, it0), prev = cur;
+  issue_copy(it0, 0);
+  load_group(it0);
+  dma_wait();
+  __syncthreads();
+  tabulate(0);
+  __syncthreads();
+  for (int it = it0; it < it1; ++it) {
+    const int bc = (it - it0) & 1, bn = bc ^ 1;
+    const bool has_next = it + 1 < it1;
+    if (has_next) issue_copy(it + 1, bn);
+    if (it > it0) store_states(prev);
+    compute(bc);
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) st_prev[q] = acc[q];
+    dma_wait();
+    __syncthreads();
+    prev = cur;
+    if (has_next) {
+      tabulate(bn);
+      const Item nxt = item_of(p, it + 1);
+      if (nxt.b != cur.b || nxt.c != cur.c || nxt.grp != cur.grp) load_group(it + 1);
+      cur = nxt;
+    }
+    __syncthreads();
+  }
+  store_states(prev);
+}
+
+template <typename T, typename S, int NK>
+hipError_t launch_nk(const ChunkStateArgs& a, hipStream_t stream) {
+  auto kern = a.dt ? chunk_state_q256_kernel<T, S, NK, true> : chunk_state_q256_kernel<T, S, NK, false>;
+  const int items = a.batch * a.nchunks * a.nheads;
+  const int grid = persistent_grid(kern, kThreads, items);
+  kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(a);
+  return hipGetLastError();
+}
+
+template <typename T, typename S>
+hipError_t launch_ts(const ChunkStateArgs& a, hipStream_t stream) {
+  switch (a.dstate) {
+    case 64: return launch_nk<T, S, 2>(a, stream);
+    case 128: return launch_nk<T, S, 4>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace
+
+bool chunk_state_persistent_supported(const ChunkStateArgs& a, int dtype) {
+  return a.chunk == kQ && (a.dstate == 64 || a.dstate == 128) &&
+         (dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16);
+}
+
+hipError_t launch_chunk_state_persistent(const ChunkStateArgs& a, int dtype, int state_dtype, hipStream_t stream) {
+  if (state_dtype == SSD_DTYPE_F32) {
+    if (dtype == SSD_DTYPE_BF16) return launch_ts<bf16, float>(a, stream);
+    if (dtype == SSD_DTYPE_F16) return launch_ts<f16, float>(a, stream);
+  } else if (state_dtype == SSD_DTYPE_BF16) {
+    if (dtype == SSD_DTYPE_BF16) return launch_ts<bf16, bf16>(a, stream);
+    if (dtype == SSD_DTYPE_F16) return launch_ts<f16, bf16>(a, stream);
+  }
+  return hipErrorInvalidValue;
+}
+
+}  // namespace ssd

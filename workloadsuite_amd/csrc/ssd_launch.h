@@ -78,6 +78,11 @@ hipError_t launch_chunk_state(const ChunkStateArgs& a, int dtype, int state_dtyp
 hipError_t launch_state_passing(const StatePassingArgs& a, int state_dtype, hipStream_t stream);
 hipError_t launch_chunk_scan(const ChunkScanArgs& a, int dtype, int state_dtype, hipStream_t stream);
 
+// chunk_state's persistent kernel for 16-bit inputs at chunk 256
+// (ssd_chunk_state_q256.hip); launch_chunk_state dispatches to it when supported.
+bool chunk_state_persistent_supported(const ChunkStateArgs& a, int dtype);
+hipError_t launch_chunk_state_persistent(const ChunkStateArgs& a, int dtype, int state_dtype, hipStream_t stream);
+
 // chunk_scan's persistent kernel for 16-bit inputs at chunk 256
 // (ssd_chunk_scan_q256.hip); launch_chunk_scan dispatches to it when supported.
 bool chunk_scan_persistent_supported(const ChunkScanArgs& a, int dtype);
