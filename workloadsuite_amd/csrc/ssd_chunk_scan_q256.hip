@@ -42,6 +42,8 @@
 //
 // Traffic per item: x 32 KB + S_in 32 KB (f32) + Acs 1 KB read, y 32 KB
 // written; B and C per group from L2.  HBM bound at this shape.
+#include <climits>
+#include <cstdint>
 #include <type_traits>
 
 #include "ssd_device.h"
@@ -60,11 +62,26 @@ constexpr int kThreads = 64 * kNW;
 constexpr int kNPair = kNT / 2 + 1;  // 32-token s blocks per wave, both tiles
 constexpr int kXBlocks = kQ / 8;     // 1 KB copy blocks of x (8 rows of 64 x 16-bit)
 
+// Kernel arguments with 32-bit element strides (offsets are still formed in
+// 64 bits): fewer scalar registers stay live across the item loop than with
+// the int64 ChunkScanArgs.  The launcher checks that every stride fits.
+struct ScanArgs32 {
+  const void* x;
+  const void* bm;
+  const void* cm;
+  const float* dt;
+  const float* acs;
+  const void* states;
+  void* y;
+  int sxb, sxl, sxh, sbb, sbl, sbg, scb, scl, scg, sdb, sdl, sdh, syb, syl, syh;
+  int batch, nchunks, nheads, ngroups, dstate;
+};
+
 struct Item {
   int b, c, h, grp;
 };
 
-__device__ __forceinline__ Item item_of(const ChunkScanArgs& p, int it) {
+__device__ __forceinline__ Item item_of(const ScanArgs32& p, int it) {
   Item r;
   r.h = it % p.nheads;
   const int bc = it / p.nheads;
@@ -76,7 +93,7 @@ __device__ __forceinline__ Item item_of(const ChunkScanArgs& p, int it) {
 
 template <typename T, typename S, int NK, bool HAS_DT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void chunk_scan_q256_kernel(ChunkScanArgs p) {
+void chunk_scan_q256_kernel(ScanArgs32 p) {
   constexpr int N = 32 * NK;                      // dstate (64 or 128)
   constexpr bool SPLIT = sizeof(S) == 4;          // f32 states become a hi/lo pair
   constexpr int LPR = N * (int)sizeof(S) / 16;    // 16-byte pieces per S_in row
@@ -122,15 +139,24 @@ void chunk_scan_q256_kernel(ChunkScanArgs p) {
   const int64_t yrow1 = (int64_t)(16 * tb + i) * p.syl + 4 * g;
 
   // ---- global -> LDS copy of one item's x, S_in, Acs (and dt) into buffer b ----
+  // LDS offsets of the buffer arrays (from the __shared__ objects themselves,
+  // so that no generic -> LDS pointer conversion is needed per copy).
+  const uint32_t xr_lds = lds_offset(&xr[0][0]), sr_lds = lds_offset(&sr[0][0]);
+  const uint32_t ar_lds = lds_offset(&ar[0][0]), dr_lds = lds_offset(&dr[0][0]);
+
   auto issue_copy = [&](int it, int b) __attribute__((always_inline)) {
+    // opaque buffer index: the LDS destinations are formed per item instead of
+    // being hoisted for both buffers (which would pin ~30 scalar registers)
+    b = __builtin_amdgcn_readfirstlane(b);
+    asm volatile("" : "+s"(b));
     const Item r = item_of(p, it);
     const int64_t l0 = (int64_t)r.c * kQ;
-    const T* xg = reinterpret_cast<const T*>(p.x) + r.b * p.sxb + l0 * p.sxl + r.h * p.sxh + xcopy;
+    const T* xg = reinterpret_cast<const T*>(p.x) + (int64_t)r.b * p.sxb + l0 * p.sxl + (int64_t)r.h * p.sxh + xcopy;
     // x: copy block blk holds rows 8 blk .. 8 blk + 7; row s keeps piece c at slot c ^ (s & 7).
 #pragma unroll
     for (int m = 0; m < kXBlocks / kNW; ++m) {
       const int blk = wave + kNW * m;
-      dma16(xg + (int64_t)(8 * blk) * p.sxl, xr[b] + blk * 512);
+      dma16_at(xg + (int64_t)(8 * blk) * p.sxl, xr_lds + (uint32_t)(b * kQ * kP * (int)sizeof(T) + blk * 1024));
     }
     // S_in: one row per copy (LPR lanes), rows ROWB bytes apart.
     const S* sg = reinterpret_cast<const S*>(p.states) +
@@ -139,20 +165,21 @@ void chunk_scan_q256_kernel(ChunkScanArgs p) {
 #pragma unroll
     for (int m = 0; m < kP / kNW; ++m) {
       const int row = wave + kNW * m;
-      const uint32_t dst = lds_offset(sr[b] + row * ROWB);
+      const uint32_t dst = sr_lds + (uint32_t)(b * kP * ROWB + row * ROWB);
       if (lane < LPR) dma16_at(sg + row * N, dst);
     }
     if (wave == kNW - 1) {
       const float* ag = p.acs + (((int64_t)r.b * p.nheads + r.h) * p.nchunks + r.c) * kQ;
-      dma16(ag + 4 * lane, ar[b]);
+      dma16_at(ag + 4 * lane, ar_lds + (uint32_t)(b * kQ * 4));
     }
     if constexpr (HAS_DT) {
       if (wave < kQ / 64) {
-        const float* dg = p.dt + r.b * p.sdb + r.h * p.sdh;
-        dma4(dg + (l0 + 64 * wave + lane) * p.sdl, dr[b] + 64 * wave);
+        const float* dg = p.dt + (int64_t)r.b * p.sdb + (int64_t)r.h * p.sdh;
+        dma4_at(dg + (l0 + 64 * wave + lane) * p.sdl, dr_lds + (uint32_t)(b * kQ * 4 + 256 * wave));
       }
     }
   };
+
 
   // ---- once the copy of buffer b has landed: Acs *= log2(e); S_in -> MFMA operand type ----
   // f32 S_in: each 32-byte pair of pieces (8 states) becomes [hi x8 | lo x8] of T in place.
@@ -202,8 +229,8 @@ void chunk_scan_q256_kernel(ChunkScanArgs p) {
     const int g = lane_o >> 4, i = lane_o & 15;
     const Item r = item_of(p, it);
     const int64_t l0 = (int64_t)r.c * kQ;
-    const T* cg = reinterpret_cast<const T*>(p.cm) + r.b * p.scb + l0 * p.scl + r.grp * p.scg;
-    const T* bg = reinterpret_cast<const T*>(p.bm) + r.b * p.sbb + l0 * p.sbl + r.grp * p.sbg;
+    const T* cg = reinterpret_cast<const T*>(p.cm) + (int64_t)r.b * p.scb + l0 * p.scl + (int64_t)r.grp * p.scg;
+    const T* bg = reinterpret_cast<const T*>(p.bm) + (int64_t)r.b * p.sbb + l0 * p.sbl + (int64_t)r.grp * p.sbg;
 #pragma unroll
     for (int kc = 0; kc < NK; ++kc) {
       cf[0][kc] = load8<T>(cg + (int64_t)(16 * ta + i) * p.scl + 32 * kc + 8 * g);
@@ -289,8 +316,13 @@ void chunk_scan_q256_kernel(ChunkScanArgs p) {
     // the block that crosses the diagonal needs the causal mask.
     auto weights = [&](int s2, int sb, const f32x4* cb, bool on_diag, const f32x4* gs) __attribute__((always_inline)) {
       frag8<T> af;
-      const int l = 16 * (s2 ? tb : ta) + i;
       if (on_diag) {
+        // The causal-mask predicates depend only on the lane: from an opaque
+        // lane id they are evaluated per item instead of being hoisted out of
+        // the item loop as ~60 live 64-bit lane masks.
+        int lane_o = lane;
+        asm volatile("" : "+v"(lane_o));
+        const int go = lane_o >> 4, l = 16 * (s2 ? tb : ta) + (lane_o & 15);
         // exact decay, masked before it can overflow above the diagonal
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
@@ -301,7 +333,7 @@ void chunk_scan_q256_kernel(ChunkScanArgs p) {
           for (int jj = 0; jj < 4; ++jj) {
             float w = __builtin_amdgcn_exp2f(al[s2] - as[jj]) * cb[st][jj];
             if constexpr (HAS_DT) w *= ds[jj];
-            af[4 * st + jj] = from_f32<T>((32 * sb + 16 * st + 4 * g + jj <= l) ? w : 0.f);
+            af[4 * st + jj] = from_f32<T>((32 * sb + 16 * st + 4 * go + jj <= l) ? w : 0.f);
           }
         }
       } else {
@@ -353,7 +385,7 @@ void chunk_scan_q256_kernel(ChunkScanArgs p) {
   };
 
   auto store_y = [&](const Item& r) __attribute__((always_inline)) {
-    T* yg = reinterpret_cast<T*>(p.y) + r.b * p.syb + ((int64_t)r.c * kQ) * p.syl + r.h * p.syh;
+    T* yg = reinterpret_cast<T*>(p.y) + (int64_t)r.b * p.syb + ((int64_t)r.c * kQ) * p.syl + (int64_t)r.h * p.syh;
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       T* yrow = yg + (s2 ? yrow1 : yrow0);
@@ -392,12 +424,32 @@ void chunk_scan_q256_kernel(ChunkScanArgs p) {
   store_y(prev);
 }
 
+bool fits_i32(int64_t v) { return v >= INT32_MIN && v <= INT32_MAX; }
+
+ScanArgs32 narrow(const ChunkScanArgs& a) {
+  ScanArgs32 n;
+  n.x = a.x;
+  n.bm = a.bm;
+  n.cm = a.cm;
+  n.dt = a.dt;
+  n.acs = a.acs;
+  n.states = a.states;
+  n.y = a.y;
+  n.sxb = (int)a.sxb, n.sxl = (int)a.sxl, n.sxh = (int)a.sxh;
+  n.sbb = (int)a.sbb, n.sbl = (int)a.sbl, n.sbg = (int)a.sbg;
+  n.scb = (int)a.scb, n.scl = (int)a.scl, n.scg = (int)a.scg;
+  n.sdb = (int)a.sdb, n.sdl = (int)a.sdl, n.sdh = (int)a.sdh;
+  n.syb = (int)a.syb, n.syl = (int)a.syl, n.syh = (int)a.syh;
+  n.batch = a.batch, n.nchunks = a.nchunks, n.nheads = a.nheads, n.ngroups = a.ngroups, n.dstate = a.dstate;
+  return n;
+}
+
 template <typename T, typename S, int NK>
 hipError_t launch_nk(const ChunkScanArgs& a, hipStream_t stream) {
   auto kern = a.dt ? chunk_scan_q256_kernel<T, S, NK, true> : chunk_scan_q256_kernel<T, S, NK, false>;
   const int items = a.batch * a.nchunks * a.nheads;
   const int grid = persistent_grid(kern, kThreads, items);
-  kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(a);
+  kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(narrow(a));
   return hipGetLastError();
 }
 
@@ -414,6 +466,9 @@ hipError_t launch_ts(const ChunkScanArgs& a, hipStream_t stream) {
 
 bool chunk_scan_persistent_supported(const ChunkScanArgs& a, int dtype) {
   // dstate 16 / 32 stay on the generic kernel (this one spills registers there).
+  for (int64_t st : {a.sxb, a.sxl, a.sxh, a.sbb, a.sbl, a.sbg, a.scb, a.scl, a.scg, a.sdb, a.sdl, a.sdh, a.syb,
+                     a.syl, a.syh})
+    if (!fits_i32(st)) return false;
   return a.chunk == kQ && (a.dstate == 64 || a.dstate == 128) &&
          (dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16);
 }

@@ -158,10 +158,10 @@ __device__ __forceinline__ f16x4 lds_read_tr(const f16* p) {
 // in flight alongside an outstanding copy (their partial vmcnt waits would
 // not count it).
 __device__ __forceinline__ uint32_t lds_offset(const void* lds) {
-  return __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)(lds_ptr<const void>)lds);
+  return (uint32_t)(uintptr_t)(lds_ptr<const void>)lds;
 }
-// As dma16, with the LDS destination already a wave-uniform LDS offset (from
-// lds_offset(), computed outside any lane-divergent branch the copy sits in).
+// As dma16, with the LDS destination given as an LDS offset (lds_offset() of
+// a __shared__ object plus a byte offset), wave-uniform.
 __device__ __forceinline__ void dma16_at(const void* g, uint32_t lds_off) {
   uint32_t saved;
   asm volatile(
@@ -171,11 +171,11 @@ __device__ __forceinline__ void dma16_at(const void* g, uint32_t lds_off) {
       "global_load_lds_dwordx4 %1, off\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "v"(g), "s"(lds_off)
+      : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_off))
       : "memory");
 }
 __device__ __forceinline__ void dma16(const void* g, void* lds_base) { dma16_at(g, lds_offset(lds_base)); }
-__device__ __forceinline__ void dma4(const void* g, void* lds_base) {
+__device__ __forceinline__ void dma4_at(const void* g, uint32_t lds_off) {
   uint32_t saved;
   asm volatile(
       "s_mov_b32 %0, m0\n\t"
@@ -184,9 +184,10 @@ __device__ __forceinline__ void dma4(const void* g, void* lds_base) {
       "global_load_lds_dword %1, off\n\t"
       "s_mov_b32 m0, %0"
       : "=&s"(saved)
-      : "v"(g), "s"(lds_offset(lds_base))
+      : "v"(g), "s"(__builtin_amdgcn_readfirstlane(lds_off))
       : "memory");
 }
+__device__ __forceinline__ void dma4(const void* g, void* lds_base) { dma4_at(g, lds_offset(lds_base)); }
 // s_waitcnt vmcnt(0): every vector memory operation of this wave has completed.
 __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
