@@ -96,11 +96,19 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void chunk_scan_q256_kernel(ScanArgs32 p) {
   constexpr int N = 32 * NK;                      // dstate (64 or 128)
   constexpr bool SPLIT = sizeof(S) == 4;          // f32 states become a hi/lo pair
-  constexpr int LPR = N * (int)sizeof(S) / 16;    // 16-byte pieces per S_in row
-  constexpr int ROWB = N * (int)sizeof(S) + 16;   // S_in row stride in LDS (padded 16 B)
+  // S_in rows in LDS: RB bytes, PPR 16-byte pieces, unpadded; piece c of row
+  // r sits at slot c ^ ssw(r), which spreads the 16 rows that one operand
+  // read touches over distinct banks.  One 64-lane copy moves RPD rows.
+  constexpr int RB = N * (int)sizeof(S);
+  constexpr int PPR = RB / 16;
+  constexpr int RPD = 1024 / RB;
+  constexpr int SCOPIES = kP / RPD / kNW;         // S_in copies per wave and item
+  static_assert(PPR >= 8 && SCOPIES >= 1 && SCOPIES <= 4, "S_in row shape");
+  auto ssw = [](int r) __attribute__((always_inline)) { return PPR >= 16 ? (r & 15) : ((r >> 1) & 7); };
   // Two buffers of each: the current item's and the next item's (in flight).
+  // After an item's compute its x buffer holds that item's y for the stores.
   __shared__ __attribute__((aligned(1024))) T xr[2][kQ * kP];
-  __shared__ __attribute__((aligned(16))) unsigned char sr[2][kP * ROWB];
+  __shared__ __attribute__((aligned(1024))) unsigned char sr[2][kP * RB];
   __shared__ __attribute__((aligned(16))) float ar[2][kQ];
   // G[s] = exp(Acs[r] - Acs[s]), r the last token of s's 32-token block
   // (written by convert(); the decay of the blocks below the diagonal factors
@@ -120,23 +128,43 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
 
   // ---- per-lane LDS offsets of the MFMA operands (fixed for the kernel) ----
   int xoff[4];  // x^T operand: rows 4g + i/4 (+ 32 sb + 16 h), columns 16 pt + 4 (i % 4), swizzled
-  int soff[4];  // S_in operand: row 16 pt + i, states 8 g .. 8 g + 7 of each 32-state K step (bytes)
+  // S_in operand, row 16 pt + i, K step kc (32 states): piece CPK kc + lp of
+  // the row, lp = 2 g (+1 for lo) when split, else g.  The slot
+  // (CPK kc + lp) ^ ssw(i) = (CPK (kc % NKB) ^ lp ^ ssw(i)) + 16 (kc / NKB)
+  // leaves NKB lane bases per half (byte offsets; + 16 pt RB per column tile).
+  constexpr int CPK = SPLIT ? 8 : 4;
+  constexpr int NKB = NK < 16 / CPK ? NK : 16 / CPK;
+  constexpr int NH = SPLIT ? 2 : 1;
+  int sbase[NKB][NH];
   {
     const int r = 4 * g + (i >> 2), x7 = r & 7;
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) {
-      xoff[pt] = r * kP + 8 * ((2 * pt + ((i & 3) >> 1)) ^ x7) + 4 * (i & 1);
-      soff[pt] = (16 * pt + i) * ROWB + g * (SPLIT ? 32 : 16);
-    }
+    for (int pt = 0; pt < 4; ++pt) xoff[pt] = r * kP + 8 * ((2 * pt + ((i & 3) >> 1)) ^ x7) + 4 * (i & 1);
+#pragma unroll
+    for (int k = 0; k < NKB; ++k)
+#pragma unroll
+      for (int h = 0; h < NH; ++h) sbase[k][h] = i * RB + 16 * ((CPK * k) ^ ((SPLIT ? 2 * g + h : g) ^ ssw(i)));
   }
 
 
   // ---- per-lane parts of the copy and store addresses (fixed for the kernel) ----
   // x copy: lane reads row (lane / 8) of its 8-row block, piece (lane % 8) ^ (lane / 8).
   const int64_t xcopy = (int64_t)(lane >> 3) * p.sxl + 8 * ((lane & 7) ^ (lane >> 3));
-  // y store: row 16 t + i, columns 16 pt + 4 g .. + 3 of each tile t.
-  const int64_t yrow0 = (int64_t)(16 * ta + i) * p.syl + 4 * g;
-  const int64_t yrow1 = (int64_t)(16 * tb + i) * p.syl + 4 * g;
+  // y staging in LDS: row l (128 B) keeps the 8 p of piece c at slot
+  // c ^ ((l >> 1) & 7).  A lane writes row 16 t + i, p 16 pt + 4 g .. + 3
+  // (8 bytes); a store copy reads 8 whole rows (1 KB, lane k: row k / 8,
+  // slot k % 8) and writes each row's 128 bytes with 16 bytes per lane.
+  // slot (2 pt + g / 2) ^ ((i >> 1) & 7) = (2 pt) ^ ysw: byte offset of column
+  // tile pt = i 128 + 8 (g & 1) + ((32 pt) ^ (16 ysw))
+  const int ysw = (g >> 1) ^ ((i >> 1) & 7);
+  const int yrow = i * 128 + 8 * (g & 1);
+  // S_in copy: lane k fills slot k % PPR of row RPD d + k / PPR, i.e. reads
+  // piece (k % PPR) ^ ssw(row); the row's ssw depends on d only through the
+  // wave (RPD d = RPD wave mod 16).
+  const int scopy = (lane / PPR) * N + ((lane % PPR) ^ ssw(wave * RPD + lane / PPR)) * (16 / (int)sizeof(S));
+  // store copy blk = wave + 8 m: rows 8 blk + lane / 8, and 8 blk is
+  // 8 wave mod 16, so the slot -> piece map depends only on the wave's parity
+  const int64_t ycopy = (int64_t)(lane >> 3) * p.syl + 8 * ((lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7));
 
   // ---- global -> LDS copy of one item's x, S_in, Acs (and dt) into buffer b ----
   // LDS offsets of the buffer arrays (from the __shared__ objects themselves,
@@ -144,41 +172,41 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   const uint32_t xr_lds = lds_offset(&xr[0][0]), sr_lds = lds_offset(&sr[0][0]);
   const uint32_t ar_lds = lds_offset(&ar[0][0]), dr_lds = lds_offset(&dr[0][0]);
 
-  auto issue_copy = [&](int it, int b) __attribute__((always_inline)) {
+  // Part `part` (0..3) of one item's copy: x block rows 64 part + 8 wave ..,
+  // S_in rows 16 part + wave and + 8; part 0 also copies Acs (and dt).  The
+  // parts are issued between compute steps, so that a wave's vector-memory
+  // queue never holds up its MFMAs for a whole item's copy.
+  auto issue_copy_part = [&](const Item& r, int b, int part) __attribute__((always_inline)) {
     // opaque buffer index: the LDS destinations are formed per item instead of
     // being hoisted for both buffers (which would pin ~30 scalar registers)
     b = __builtin_amdgcn_readfirstlane(b);
     asm volatile("" : "+s"(b));
-    const Item r = item_of(p, it);
     const int64_t l0 = (int64_t)r.c * kQ;
     const T* xg = reinterpret_cast<const T*>(p.x) + (int64_t)r.b * p.sxb + l0 * p.sxl + (int64_t)r.h * p.sxh + xcopy;
     // x: copy block blk holds rows 8 blk .. 8 blk + 7; row s keeps piece c at slot c ^ (s & 7).
-#pragma unroll
-    for (int m = 0; m < kXBlocks / kNW; ++m) {
-      const int blk = wave + kNW * m;
+    {
+      const int blk = wave + kNW * part;
       dma16_at(xg + (int64_t)(8 * blk) * p.sxl, xr_lds + (uint32_t)(b * kQ * kP * (int)sizeof(T) + blk * 1024));
     }
-    // S_in: one row per copy (LPR lanes), rows ROWB bytes apart.
-    const S* sg = reinterpret_cast<const S*>(p.states) +
-                  (((int64_t)r.b * p.nchunks + r.c) * p.nheads + r.h) * (int64_t)(kP * N) +
-                  lane * (16 / (int)sizeof(S));
-#pragma unroll
-    for (int m = 0; m < kP / kNW; ++m) {
-      const int row = wave + kNW * m;
-      const uint32_t dst = sr_lds + (uint32_t)(b * kP * ROWB + row * ROWB);
-      if (lane < LPR) dma16_at(sg + row * N, dst);
+    // S_in: copy d = wave + 8 part moves rows RPD d .. RPD d + RPD - 1 (1 KB).
+    if (part < SCOPIES) {
+      const S* sg = reinterpret_cast<const S*>(p.states) +
+                    (((int64_t)r.b * p.nchunks + r.c) * p.nheads + r.h) * (int64_t)(kP * N) + scopy;
+      const int d = wave + kNW * part;
+      dma16_at(sg + d * RPD * N, sr_lds + (uint32_t)(b * kP * RB + d * 1024));
     }
-    if (wave == kNW - 1) {
+    if (part == 0 && wave == kNW - 1) {
       const float* ag = p.acs + (((int64_t)r.b * p.nheads + r.h) * p.nchunks + r.c) * kQ;
       dma16_at(ag + 4 * lane, ar_lds + (uint32_t)(b * kQ * 4));
     }
     if constexpr (HAS_DT) {
-      if (wave < kQ / 64) {
+      if (part == 0 && wave < kQ / 64) {
         const float* dg = p.dt + (int64_t)r.b * p.sdb + (int64_t)r.h * p.sdh;
         dma4_at(dg + (l0 + 64 * wave + lane) * p.sdl, dr_lds + (uint32_t)(b * kQ * 4 + 256 * wave));
       }
     }
   };
+  static_assert(kXBlocks == 4 * kNW, "four copy parts cover x");
 
 
   // ---- once the copy of buffer b has landed: Acs *= log2(e); S_in -> MFMA operand type ----
@@ -193,10 +221,12 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     for (int e = tid; e < kQ; e += kThreads) ar[b][e] *= kLog2e;
     if constexpr (SPLIT) {
       for (int u = tid; u < kP * (N / 8); u += kThreads) {
-        const int row = u / (N / 8), q = u % (N / 8);
-        unsigned char* pr = sr[b] + row * ROWB + 32 * q;
-        const f32x4 v0 = *reinterpret_cast<const f32x4*>(pr);
-        const f32x4 v1 = *reinterpret_cast<const f32x4*>(pr + 16);
+        // pair q = pieces 2q, 2q+1 (8 states) -> hi at piece 2q's slot, lo at 2q+1's
+        const int row = u / (N / 8), q = u % (N / 8), sw = ssw(row);
+        unsigned char* ph = sr[b] + row * RB + 16 * ((2 * q) ^ sw);
+        unsigned char* pl = sr[b] + row * RB + 16 * ((2 * q + 1) ^ sw);
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(ph);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(pl);
         frag8<T> hi, lo;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -205,12 +235,12 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
           hi[4 + k] = from_f32<T>(v1[k]);
           lo[4 + k] = from_f32<T>(v1[k] - to_f32<T>(hi[4 + k]));
         }
-        *reinterpret_cast<frag8<T>*>(pr) = hi;
-        *reinterpret_cast<frag8<T>*>(pr + 16) = lo;
+        *reinterpret_cast<frag8<T>*>(ph) = hi;
+        *reinterpret_cast<frag8<T>*>(pl) = lo;
       }
     } else if constexpr (!std::is_same<S, T>::value) {
-      for (int u = tid; u < kP * LPR; u += kThreads) {
-        unsigned char* pr = sr[b] + (u / LPR) * ROWB + 16 * (u % LPR);
+      for (int u = tid; u < kP * PPR; u += kThreads) {
+        unsigned char* pr = sr[b] + 16 * u;
         const frag8<S> v = *reinterpret_cast<const frag8<S>*>(pr);
         frag8<T> o;
 #pragma unroll
@@ -272,7 +302,8 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   // block, so its x^T fragments and G factors are read once and feed two
   // independent MFMA chains.
   vec4<T> ypk[2][4];
-  auto compute = [&](int b) __attribute__((always_inline)) {
+  // off_step(pt) runs before off-diagonal step pt.
+  auto compute = [&](int b, auto off_step) __attribute__((always_inline)) {
     const T* xb = xr[b];
     const unsigned char* sbuf = sr[b];
     const float* ab = ar[b];
@@ -291,14 +322,15 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     // off-diagonal: acc[s2][pt] = S_in[p, :] . C[l, :], then * exp(Acs[l])
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) {
+      off_step(pt);
 #pragma unroll
       for (int kc = 0; kc < NK; ++kc) {
-        const unsigned char* q = sbuf + soff[pt] + kc * (SPLIT ? 128 : 64);
-        const frag8<T> hi = *reinterpret_cast<const frag8<T>*>(q);
+        const unsigned char* q = sbuf + 16 * pt * RB + 256 * (kc / NKB);
+        const frag8<T> hi = *reinterpret_cast<const frag8<T>*>(q + sbase[kc % NKB][0]);
         acc[0][pt] = mma(hi, cf[0][kc], acc[0][pt]);
         acc[1][pt] = mma(hi, cf[1][kc], acc[1][pt]);
         if constexpr (SPLIT) {
-          const frag8<T> lo = *reinterpret_cast<const frag8<T>*>(q + 16);
+          const frag8<T> lo = *reinterpret_cast<const frag8<T>*>(q + sbase[kc % NKB][NH - 1]);
           acc[0][pt] = mma(lo, cf[0][kc], acc[0][pt]);
           acc[1][pt] = mma(lo, cf[1][kc], acc[1][pt]);
         }
@@ -384,21 +416,32 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
         for (int jj = 0; jj < 4; ++jj) ypk[s2][pt][jj] = from_f32<T>(acc[s2][pt][jj]);
   };
 
-  auto store_y = [&](const Item& r) __attribute__((always_inline)) {
-    T* yg = reinterpret_cast<T*>(p.y) + (int64_t)r.b * p.syb + ((int64_t)r.c * kQ) * p.syl + (int64_t)r.h * p.syh;
+  // y through LDS: stage_y writes this wave's rows into x buffer b (free once
+  // every wave has computed from it); store_y(r, b, m) reads store copy m
+  // (rows 8 (wave + 8 m) .. + 7) back and writes it to item r's y.
+  auto stage_y = [&](int b) __attribute__((always_inline)) {
+    unsigned char* xb = reinterpret_cast<unsigned char*>(xr[b]);
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      T* yrow = yg + (s2 ? yrow1 : yrow0);
-#pragma unroll
-      for (int pt = 0; pt < 4; ++pt) store4<T>(yrow + 16 * pt, ypk[s2][pt]);
+    for (int pt = 0; pt < 4; ++pt) {
+      const int o = yrow + ((32 * pt) ^ (16 * ysw));
+      *reinterpret_cast<vec4<T>*>(xb + 2048 * ta + o) = ypk[0][pt];
+      *reinterpret_cast<vec4<T>*>(xb + 2048 * tb + o) = ypk[1][pt];
     }
   };
+  auto store_y = [&](const Item& r, int b, int m) __attribute__((always_inline)) {
+    const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr[b]);
+    const frag8<T> v = *reinterpret_cast<const frag8<T>*>(xb + (wave + kNW * m) * 1024 + 16 * lane);
+    T* yg = reinterpret_cast<T*>(p.y) + (int64_t)r.b * p.syb + ((int64_t)r.c * kQ) * p.syl + (int64_t)r.h * p.syh;
+    *reinterpret_cast<frag8<T>*>(yg + (int64_t)(8 * (wave + kNW * m)) * p.syl + ycopy) = v;
+  };
 
-  // Per item: start the next item's copy, store the previous item's y,
-  // compute this one; then wait for the copy, publish it, convert it, and
-  // publish the conversion.
+  // Per item: compute it while the previous item's staged y is stored and
+  // the next item's copy issued (into the same LDS blocks, each read out by
+  // its wave first) between its steps; then wait for the copy, publish it,
+  // stage this item's y, convert the copy, and publish both.
   Item cur = item_of(p, it0), prev = cur;
-  issue_copy(it0, 0);
+#pragma unroll
+  for (int part = 0; part < 4; ++part) issue_copy_part(cur, 0, part);
   load_group(it0);
   dma_wait();
   __syncthreads();
@@ -407,21 +450,27 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   for (int it = it0; it < it1; ++it) {
     const int bc = (it - it0) & 1, bn = bc ^ 1;
     const bool has_next = it + 1 < it1;
-    if (has_next) issue_copy(it + 1, bn);
-    if (it > it0) store_y(prev);
-    compute(bc);
+    const Item nxt = has_next ? item_of(p, it + 1) : cur;
+    const bool has_prev = it > it0;
+    compute(bc, [&](int pt) __attribute__((always_inline)) {
+      if (has_prev) store_y(prev, bn, pt);
+      // block wave + 8 pt is read out before the copy into it is issued
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      if (has_next) issue_copy_part(nxt, bn, pt);
+    });
     dma_wait();
     __syncthreads();
+    stage_y(bc);
     prev = cur;
     if (has_next) {
       convert(bn);
-      const Item nxt = item_of(p, it + 1);
       if (nxt.b != cur.b || nxt.c != cur.c || nxt.grp != cur.grp) load_group(it + 1);
       cur = nxt;
     }
     __syncthreads();
   }
-  store_y(prev);
+#pragma unroll
+  for (int m = 0; m < 4; ++m) store_y(prev, (it1 - 1 - it0) & 1, m);
 }
 
 bool fits_i32(int64_t v) { return v >= INT32_MIN && v <= INT32_MAX; }
@@ -469,6 +518,8 @@ bool chunk_scan_persistent_supported(const ChunkScanArgs& a, int dtype) {
   for (int64_t st : {a.sxb, a.sxl, a.sxh, a.sbb, a.sbl, a.sbg, a.scb, a.scl, a.scg, a.sdb, a.sdl, a.sdh, a.syb,
                      a.syl, a.syh})
     if (!fits_i32(st)) return false;
+  // y is written 16 bytes per lane
+  if (reinterpret_cast<uintptr_t>(a.y) % 16 != 0 || a.syb % 8 != 0 || a.syl % 8 != 0 || a.syh % 8 != 0) return false;
   return a.chunk == kQ && (a.dstate == 64 || a.dstate == 128) &&
          (dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16);
 }
