@@ -4,8 +4,8 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3]
                     [--state-dtype f32|bf16] [--no-cpu-baseline]
 
-A step is one SSD forward (K1 cumsum -> K2 chunk_state -> K3 state_passing ->
-K4 chunk_scan) over one batch of synthetic inputs already resident in HBM, at
+A step is one SSD forward (K1 cumsum -> K0 chunk_prep -> K2 chunk_state ->
+K3 state_passing -> K4 chunk_scan) over one batch of synthetic inputs already resident in HBM, at
 the Mamba-2-2.7B layer shape by default (C3: batch 4, seqlen 4096, 80 heads,
 head_dim 64, d_state 128, chunk 256, 1 group, bf16 X/B/C, fp32 A, final state
 returned).  Prints ONE JSON line.
@@ -66,8 +66,11 @@ def kernel_model(cfg, state_dtype):
     fin = b * h * P * N * 4 if cfg.final_state else 0
     init = b * h * P * N * 4 if cfg.init_state else 0
     TQ = Q * (Q + 1) // 2
+    cb_frag = b * c * g * 8 * 9 * 2 * 64 * 16       # chunk_prep's CB^T fragments (f32)
+    bt_frag = b * c * g * (N // 16) * 8 * 64 * 16   # and B^T fragments (16-bit)
     return {
         "chunk_cumsum": dict(bytes=a + acs + dec, flops=b * L * h),
+        "chunk_prep": dict(bytes=2 * bc + cb_frag + bt_frag, flops=2 * b * c * g * TQ * N),
         "chunk_state": dict(bytes=x + bc + acs + st, flops=2 * b * c * h * Q * P * N),
         "state_passing": dict(bytes=2 * st + dec + fin + init, flops=2 * b * c * h * P * N),
         "chunk_scan": dict(bytes=x + 2 * bc + acs + st + x,
@@ -209,18 +212,26 @@ def main():
 
     # ---- per-kernel device time, each kernel on its real inputs ----
     Acs, decay = S.chunk_cumsum(A, cfg.chunk)
-    states = S.chunk_state(X, B, Acs, state_dtype=state_dtype)
-    S_in, _ = S.state_passing(states, decay, init)
-    # K3 is timed in place on its own buffer (re-applying the recurrence to its
-    # output each launch: same traffic, values stay finite at these decays).
-    sp_buf = S_in.clone()
+    prep = S.chunk_prep(B, C, cfg.chunk)
+    states = S.chunk_state(X, B, Acs, state_dtype=state_dtype, prep=prep)
+    # as in ssd_forward: with prep (chunk 256, 16-bit inputs) and f32 states, K3
+    # hands S_in to K4 as 16-bit (hi, lo) pairs
+    split = cfg.dtype if (prep is not None and state_dtype == torch.float32) else None
+    S_in, _ = S.state_passing(states, decay, init, split=split)
+    # K3 is timed in place on its own buffer, re-applying the recurrence to its
+    # own output on every launch: the same traffic and instructions (nothing in
+    # the kernel depends on the values, which stop being meaningful).
+    sp_buf = states.clone()
     sp_final = torch.empty(cfg.batch, cfg.nheads, cfg.headdim, cfg.dstate, device=dev) if cfg.final_state else None
     kfn = {
         "chunk_cumsum": lambda: S.chunk_cumsum(A, cfg.chunk),
-        "chunk_state": lambda: S.chunk_state(X, B, Acs, state_dtype=state_dtype),
-        "state_passing": lambda: S.state_passing_(sp_buf, decay, init, sp_final),
-        "chunk_scan": lambda: S.chunk_scan(X, B, C, Acs, S_in),
+        "chunk_prep": lambda: S.chunk_prep(B, C, cfg.chunk),
+        "chunk_state": lambda: S.chunk_state(X, B, Acs, state_dtype=state_dtype, prep=prep),
+        "state_passing": lambda: S.state_passing_(sp_buf, decay, init, sp_final, split=split),
+        "chunk_scan": lambda: S.chunk_scan(X, B, C, Acs, S_in, prep=prep, split=split is not None),
     }
+    if prep is None:
+        del kfn["chunk_prep"]
     model = kernel_model(cfg, state_dtype)
     kernels = {}
     for name, fn in kfn.items():

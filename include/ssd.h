@@ -41,13 +41,21 @@
 extern "C" {
 #endif
 
-#define SSD_ABI_VERSION 1
+#define SSD_ABI_VERSION 2
 
-/* Element types. */
+/* Element types.  The two SPLIT values are a storage format of the per-chunk
+ * states only: each f32 state as the 16-bit pair hi = round(v),
+ * lo = round(v - hi) of the inputs' type, stored per 8 consecutive states as
+ * [hi x8 | lo x8] (4 bytes per state, as f32).  ssd_state_passing writes it
+ * from f32 local states; ssd_chunk_scan reads it, for 16-bit inputs of that
+ * type at chunk 256 and dstate 64 / 128, as MFMA operands without converting
+ * it.  ssd_forward uses it internally. */
 enum {
   SSD_DTYPE_F32 = 0,
   SSD_DTYPE_BF16 = 1,
   SSD_DTYPE_F16 = 2,
+  SSD_STATE_SPLIT_BF16 = 3,
+  SSD_STATE_SPLIT_F16 = 4,
 };
 
 /* Status codes (negative: rejected on the host before any launch). */
@@ -88,9 +96,10 @@ const char* ssd_strerror(int status);
  * errors MR raises (MR:37-38 ValueError, MR:106-110 einops error). */
 int ssd_check_dims(const ssd_dims* d, int dtype);
 
-/* Bytes of workspace ssd_forward needs: a_cumsum, chunk_decay and the
- * per-chunk states (state_dtype: SSD_DTYPE_F32 or SSD_DTYPE_BF16), each
- * region 256-byte aligned.  0 when dims are invalid. */
+/* Bytes of workspace ssd_forward needs: a_cumsum, chunk_decay, the
+ * per-chunk states (state_dtype: SSD_DTYPE_F32 or SSD_DTYPE_BF16) and
+ * ssd_chunk_prep_bytes(d), each region 256-byte aligned.  0 when dims are
+ * invalid. */
 size_t ssd_workspace_bytes(const ssd_dims* d, int state_dtype);
 
 /* K1 -- intra-chunk cumsum of the log-decays and the per-chunk total decay.
@@ -99,15 +108,33 @@ size_t ssd_workspace_bytes(const ssd_dims* d, int state_dtype);
 int ssd_chunk_cumsum(const ssd_dims* d, const float* a, const int64_t a_strides[3],
                      float* a_cumsum, float* chunk_decay, void* stream);
 
+/* K0 -- per-(batch, chunk, group) operands of the chunk-256 kernels for
+ * 16-bit inputs: C.B^T over each chunk (MR:143) in the register order
+ * ssd_chunk_scan keeps it in, and B in the order ssd_chunk_state keeps it in.
+ * Optional: K2 / K4 given prep = NULL rebuild them on every CU that meets a
+ * group, which costs a chain of dependent loads per group.
+ * ssd_chunk_prep_bytes is 0 for shapes without that path (chunk != 256 or
+ * dstate not 64 / 128); ssd_chunk_prep then returns SSD_OK and writes
+ * nothing, as it does for f32 inputs.  prep: device memory, 256-byte
+ * aligned.  MR forms C.B^T inside its einsum (MR:143); there is no separate
+ * reference interface for this stage. */
+size_t ssd_chunk_prep_bytes(const ssd_dims* d);
+int ssd_chunk_prep(const ssd_dims* d, int dtype,
+                   const void* bmat, const int64_t b_strides[4],
+                   const void* cmat, const int64_t c_strides[4],
+                   void* prep, size_t prep_bytes, void* stream);
+
 /* K2 -- per-chunk local states
  *   states[b,c,h,p,n] = sum_l x[l,p] dt[l] exp(Acs[Q-1]-Acs[l]) bmat[l,n].
  * Replaces MR:144 (X*dt) and MR:148-149 (decay_to_end and the 3-operand
- * einsum).  MR's [.., N, P] state is stored here as [.., P, N]. */
+ * einsum).  MR's [.., N, P] state is stored here as [.., P, N].
+ * prep: NULL, or ssd_chunk_prep's output for the same d, dtype and bmat. */
 int ssd_chunk_state(const ssd_dims* d, int dtype,
                     const void* x, const int64_t x_strides[4],
                     const void* bmat, const int64_t b_strides[4],
                     const float* dt, const int64_t dt_strides[3],
-                    const float* a_cumsum, void* states, int state_dtype, void* stream);
+                    const float* a_cumsum, void* states, int state_dtype,
+                    const void* prep, void* stream);
 
 /* K3 -- inter-chunk recurrence, in place: on entry states[c] holds chunk c's
  * local state, on exit the state entering chunk c:
@@ -122,16 +149,18 @@ int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype,
  *   y[l,p] = sum_{s<=l} exp(Acs[l]-Acs[s]) (C_l.B_s) dt[s] x[s,p]
  *            + exp(Acs[l]) sum_n C[l,n] states[c][p,n].
  * Replaces MR:139-145 (segsum, mask, C.B^T, Y_diag), MR:160-161 (Y_off) and
- * MR:162 (the sum). */
+ * MR:162 (the sum).
+ * prep: NULL, or ssd_chunk_prep's output for the same d, dtype, bmat, cmat. */
 int ssd_chunk_scan(const ssd_dims* d, int dtype,
                    const void* x, const int64_t x_strides[4],
                    const void* bmat, const int64_t b_strides[4],
                    const void* cmat, const int64_t c_strides[4],
                    const float* dt, const int64_t dt_strides[3],
                    const float* a_cumsum, const void* states, int state_dtype,
-                   void* y, const int64_t y_strides[4], void* stream);
+                   void* y, const int64_t y_strides[4],
+                   const void* prep, void* stream);
 
-/* Whole SSD forward (K1..K4 on one stream): the replacement for
+/* Whole SSD forward (K1, K0, K2, K3, K4 on one stream): the replacement for
  * SSDLayer._ssd_core (MR:123-162).  workspace must hold
  * ssd_workspace_bytes(d, state_dtype) bytes, 256-byte aligned. */
 int ssd_forward(const ssd_dims* d, int dtype,

@@ -80,6 +80,12 @@ def test_workspace_bytes_layout():
     assert n32 - n16 == states32 // 2
     bad = d(seqlen=100)
     assert lib.ssd_workspace_bytes(ctypes.byref(bad), _lib.DTYPE_F32) == 0
+    # chunk 256, dstate 128: also chunk_prep's CB^T fragments (8 waves x 9 steps
+    # x 2 sub-tiles x 1 KB) and B^T fragments (8 n tiles x 8 steps x 1 KB) per group
+    big = d(seqlen=1024, chunk=256, dstate=128, ngroups=2)
+    groups = 2 * 4 * 2
+    base = 2 * 8 * 4 * (256 * 4 + 4 + 64 * 128 * 4)
+    assert lib.ssd_workspace_bytes(ctypes.byref(big), _lib.DTYPE_F32) >= base + groups * (144 + 64) * 1024
 
 
 def test_entry_points_reject_null_and_bad_strides_before_launch():
@@ -90,23 +96,32 @@ def test_entry_points_reject_null_and_bad_strides_before_launch():
     bs4 = (ctypes.c_int64 * 4)(256 * 2 * 64, 2 * 64, 64, 1)
     fake = ctypes.c_void_p(0x100000)  # never dereferenced: validation fails first
     # null x
-    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, None, s4, fake, bs4, None, None, fake, fake, 0, None) == -1
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, None, s4, fake, bs4, None, None, fake, fake, 0, None, None) == -1
     # inner stride != 1
     bad = (ctypes.c_int64 * 4)(256 * 8 * 64, 8 * 64, 1, 8)
-    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, fake, bad, fake, bs4, None, None, fake, fake, 0, None) == -9
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, fake, bad, fake, bs4, None, None, fake, fake, 0, None, None) == -9
     # misaligned base pointer
     mis = ctypes.c_void_p(0x100002)
-    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, mis, s4, fake, bs4, None, None, fake, fake, 0, None) == -10
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, mis, s4, fake, bs4, None, None, fake, fake, 0, None, None) == -10
     # row stride not a multiple of 16 bytes
     odd = (ctypes.c_int64 * 4)(256 * 8 * 64, 8 * 64 + 3, 64, 1)
-    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, fake, odd, fake, bs4, None, None, fake, fake, 0, None) == -10
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, fake, odd, fake, bs4, None, None, fake, fake, 0, None, None) == -10
     # bf16 states with f32 inputs are not supported
-    assert lib.ssd_chunk_state(ctypes.byref(dims), 0, fake, s4, fake, bs4, None, None, fake, fake, 1, None) == -5
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 0, fake, s4, fake, bs4, None, None, fake, fake, 1, None, None) == -5
     # workspace too small / misaligned
     assert lib.ssd_forward(ctypes.byref(dims), 1, fake, s4, fake, s3, fake, bs4, fake, bs4, None, None, None,
                            fake, s4, None, fake, 16, 0, None) == -11
     assert lib.ssd_forward(ctypes.byref(dims), 1, fake, s4, fake, s3, fake, bs4, fake, bs4, None, None, None,
                            fake, s4, None, ctypes.c_void_p(0x100010), 1 << 30, 0, None) == -10
+    # chunk_prep: nothing to do for f32 inputs or chunk 64; otherwise checked like a workspace
+    big = d(seqlen=512, chunk=256, dstate=128)
+    n = lib.ssd_chunk_prep_bytes(ctypes.byref(big))
+    assert n > 0 and lib.ssd_chunk_prep_bytes(ctypes.byref(dims)) == 0
+    assert lib.ssd_chunk_prep(ctypes.byref(big), 0, fake, bs4, fake, bs4, None, 0, None) == 0
+    assert lib.ssd_chunk_prep(ctypes.byref(dims), 1, fake, bs4, fake, bs4, None, 0, None) == 0
+    assert lib.ssd_chunk_prep(ctypes.byref(big), 1, fake, bs4, fake, bs4, None, n, None) == -1
+    assert lib.ssd_chunk_prep(ctypes.byref(big), 1, fake, bs4, fake, bs4, ctypes.c_void_p(0x100010), n, None) == -10
+    assert lib.ssd_chunk_prep(ctypes.byref(big), 1, fake, bs4, fake, bs4, fake, n - 256, None) == -11
     # state passing: misaligned initial state
     assert lib.ssd_state_passing(ctypes.byref(dims), fake, 0, fake, ctypes.c_void_p(0x100004), None, None) == -10
 

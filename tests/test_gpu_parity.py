@@ -187,6 +187,36 @@ def test_forward_bf16_states():
     assert_close(final, fs, 2e-2)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("N,h,g,use_dt", [(128, 24, 2, False), (64, 12, 3, True), (128, 10, 5, True)])
+def test_forward_equals_kernel_by_kernel(dtype, N, h, g, use_dt):
+    """ssd_forward (chunk_prep's precomputed group operands) against the four
+    public kernels called one by one (each CU rebuilds them): bit-identical.
+    More items than CUs and few heads per group, so ranges cross groups."""
+    say("fwd == kernels", dtype, N, h, g, use_dt)
+    cfg, inp = small_case(dtype, 256, N, b=4, nc=16, h=h, g=g)
+    d = to_dev(inp)
+    dt = torch.rand(4, 16 * 256, h, device=DEV) + 0.5 if use_dt else None
+    Y, final = S.ssd_forward(d["X"], d["A"], d["B"], d["C"], 256, dt=dt, return_final_states=True)
+    Acs, dec = S.chunk_cumsum(d["A"], 256)
+    st = S.chunk_state(d["X"], d["B"], Acs, dt=dt)
+    S_in, fin = S.state_passing(st, dec)
+    Yk = S.chunk_scan(d["X"], d["B"], d["C"], Acs, S_in, dt=dt)
+    prep = S.chunk_prep(d["B"], d["C"], 256)
+    assert prep is not None
+    assert torch.equal(S.chunk_state(d["X"], d["B"], Acs, dt=dt, prep=prep), st)
+    Yp = S.chunk_scan(d["X"], d["B"], d["C"], Acs, S_in, dt=dt, prep=prep)
+    # the forward's own K3 -> K4 hand-over: S_in stored as (hi, lo) pairs
+    S_sp, fin_sp = S.state_passing(st, dec, split=dtype)
+    Ys = S.chunk_scan(d["X"], d["B"], d["C"], Acs, S_sp, dt=dt, prep=prep, split=True)
+    torch.cuda.synchronize()
+    assert torch.equal(Y, Yk)
+    assert torch.equal(Yp, Yk)
+    assert torch.equal(Ys, Yk)
+    assert torch.equal(final, fin)
+    assert torch.equal(fin_sp, fin)
+
+
 # ---------------------------------------------------------------------------
 # benchmark configurations at full size
 # ---------------------------------------------------------------------------

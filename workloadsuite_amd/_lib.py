@@ -15,8 +15,9 @@ import torch  # noqa: F401  -- must precede the CDLL, see module docstring
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssd.so")
 
-SSD_ABI_VERSION = 1
+SSD_ABI_VERSION = 2
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
+STATE_SPLIT_BF16, STATE_SPLIT_F16 = 3, 4  # f32 states as 16-bit (hi, lo) pairs
 
 # Every symbol include/ssd.h declares.
 EXPORTS = (
@@ -24,6 +25,8 @@ EXPORTS = (
     "ssd_strerror",
     "ssd_check_dims",
     "ssd_workspace_bytes",
+    "ssd_chunk_prep_bytes",
+    "ssd_chunk_prep",
     "ssd_chunk_cumsum",
     "ssd_chunk_state",
     "ssd_state_passing",
@@ -48,10 +51,12 @@ _SIGNATURES = {
     "ssd_check_dims": (_int, [_dims_p, _int]),
     "ssd_workspace_bytes": (ctypes.c_size_t, [_dims_p, _int]),
     "ssd_chunk_cumsum": (_int, [_dims_p, _vp, _i64p, _vp, _vp, _vp]),
-    "ssd_chunk_state": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _int, _vp]),
+    "ssd_chunk_prep_bytes": (ctypes.c_size_t, [_dims_p]),
+    "ssd_chunk_prep": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, ctypes.c_size_t, _vp]),
+    "ssd_chunk_state": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _int, _vp, _vp]),
     "ssd_state_passing": (_int, [_dims_p, _vp, _int, _vp, _vp, _vp, _vp]),
     "ssd_chunk_scan": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
-                              _vp, _vp, _int, _vp, _i64p, _vp]),
+                              _vp, _vp, _int, _vp, _i64p, _vp, _vp]),
     "ssd_forward": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                            _vp, _vp, _i64p, _vp, _vp, ctypes.c_size_t, _int, _vp]),
 }

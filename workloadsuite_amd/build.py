@@ -24,6 +24,7 @@ ARCH = "gfx950"
 SOURCES = [
     "ssd_api.cpp",
     "ssd_cumsum.hip",
+    "ssd_chunk_prep.hip",
     "ssd_chunk_state.hip",
     "ssd_chunk_state_q256.hip",
     "ssd_state_passing.hip",

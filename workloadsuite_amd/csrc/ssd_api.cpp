@@ -12,6 +12,7 @@
 
 namespace {
 
+using ssd::ChunkPrepArgs;
 using ssd::ChunkScanArgs;
 using ssd::ChunkStateArgs;
 using ssd::CumsumArgs;
@@ -29,6 +30,13 @@ bool valid_dtype(int dtype) {
 bool valid_state_dtype(int dtype, int state_dtype) {
   if (state_dtype == SSD_DTYPE_F32) return true;
   return state_dtype == SSD_DTYPE_BF16 && dtype != SSD_DTYPE_F32;
+}
+
+// The 16-bit type of a SPLIT state storage, 0 for the others.
+int split_of(int state_dtype) {
+  if (state_dtype == SSD_STATE_SPLIT_BF16) return SSD_DTYPE_BF16;
+  if (state_dtype == SSD_STATE_SPLIT_F16) return SSD_DTYPE_F16;
+  return 0;
 }
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
@@ -92,8 +100,22 @@ int hip_status(hipError_t e) { return e == hipSuccess ? SSD_OK : (int)e; }
 size_t round_up(size_t v) { return (v + kWsAlign - 1) / kWsAlign * kWsAlign; }
 
 struct WsLayout {
-  size_t acs, decay, states, total;
+  size_t acs, decay, states, prep, total;
 };
+
+// chunk_prep's outputs only exist for the persistent kernels' shapes
+bool prep_shape(const ssd_dims* d) { return d->chunk == 256 && (d->dstate == 64 || d->dstate == 128); }
+
+// prep buffer: the CB^T fragments, then (256-byte aligned) the B^T fragments
+size_t prep_cb_region(const ssd_dims* d) {
+  const int64_t groups = d->batch * (d->seqlen / d->chunk) * d->ngroups;
+  return round_up(ssd::chunk_prep_cb_bytes(groups));
+}
+size_t prep_bytes(const ssd_dims* d) {
+  if (!prep_shape(d)) return 0;
+  const int64_t groups = d->batch * (d->seqlen / d->chunk) * d->ngroups;
+  return prep_cb_region(d) + round_up(ssd::chunk_prep_bt_bytes(groups, (int)d->dstate));
+}
 
 WsLayout ws_layout(const ssd_dims* d, int state_dtype) {
   const size_t nchunks = (size_t)(d->seqlen / d->chunk);
@@ -102,8 +124,119 @@ WsLayout ws_layout(const ssd_dims* d, int state_dtype) {
   w.acs = 0;
   w.decay = round_up(bhc * (size_t)d->chunk * sizeof(float));
   w.states = w.decay + round_up(bhc * sizeof(float));
-  w.total = w.states + round_up(bhc * (size_t)d->headdim * d->dstate * elem_size(state_dtype));
+  w.prep = w.states + round_up(bhc * (size_t)d->headdim * d->dstate * elem_size(state_dtype));
+  w.total = w.prep + prep_bytes(d);
   return w;
+}
+
+ChunkPrepArgs make_prep_args(const ssd_dims* d, const void* bmat, const int64_t b_strides[4], const void* cmat,
+                             const int64_t c_strides[4], void* prep) {
+  ChunkPrepArgs pa;
+  pa.bm = bmat;
+  pa.sbb = b_strides[0];
+  pa.sbl = b_strides[1];
+  pa.sbg = b_strides[2];
+  pa.cm = cmat;
+  pa.scb = c_strides[0];
+  pa.scl = c_strides[1];
+  pa.scg = c_strides[2];
+  pa.batch = (int)d->batch;
+  pa.nchunks = (int)(d->seqlen / d->chunk);
+  pa.ngroups = (int)d->ngroups;
+  pa.dstate = (int)d->dstate;
+  pa.chunk = (int)d->chunk;
+  pa.cbf = reinterpret_cast<float*>(prep);
+  pa.btf = static_cast<char*>(prep) + prep_cb_region(d);
+  return pa;
+}
+
+StatePassingArgs make_sp_args(const ssd_dims* d, void* states, const float* chunk_decay,
+                              const float* initial_states, float* final_states) {
+  StatePassingArgs p;
+  p.states = states;
+  p.decay = chunk_decay;
+  p.init = initial_states;
+  p.final_state = final_states;
+  p.batch = (int)d->batch;
+  p.nchunks = (int)(d->seqlen / d->chunk);
+  p.nheads = (int)d->nheads;
+  p.headdim = (int)d->headdim;
+  p.dstate = (int)d->dstate;
+  return p;
+}
+
+// The CB^T / B^T fragments inside a prep buffer (null when there is none).
+const float* prep_cbf(const void* prep) { return static_cast<const float*>(prep); }
+const void* prep_btf(const ssd_dims* d, const void* prep) {
+  return prep ? static_cast<const char*>(prep) + prep_cb_region(d) : nullptr;
+}
+
+// A 16-bit input with a prepared shape: ssd_chunk_prep has work to do.
+bool prep_applies(const ssd_dims* d, int dtype) {
+  return prep_shape(d) && (dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16);
+}
+
+ChunkStateArgs make_state_args(const ssd_dims* d, const void* x, const int64_t x_strides[4], const void* bmat,
+                               const int64_t b_strides[4], const float* dt, const int64_t dt_strides[3],
+                               const float* a_cumsum, void* states) {
+  ChunkStateArgs p;
+  p.x = x;
+  p.sxb = x_strides[0];
+  p.sxl = x_strides[1];
+  p.sxh = x_strides[2];
+  p.bm = bmat;
+  p.sbb = b_strides[0];
+  p.sbl = b_strides[1];
+  p.sbg = b_strides[2];
+  p.dt = dt;
+  p.sdb = dt ? dt_strides[0] : 0;
+  p.sdl = dt ? dt_strides[1] : 0;
+  p.sdh = dt ? dt_strides[2] : 0;
+  p.acs = a_cumsum;
+  p.states = states;
+  p.batch = (int)d->batch;
+  p.nchunks = (int)(d->seqlen / d->chunk);
+  p.nheads = (int)d->nheads;
+  p.ngroups = (int)d->ngroups;
+  p.dstate = (int)d->dstate;
+  p.chunk = (int)d->chunk;
+  return p;
+}
+
+ChunkScanArgs make_scan_args(const ssd_dims* d, const void* x, const int64_t x_strides[4], const void* bmat,
+                             const int64_t b_strides[4], const void* cmat, const int64_t c_strides[4],
+                             const float* dt, const int64_t dt_strides[3], const float* a_cumsum,
+                             const void* states, void* y, const int64_t y_strides[4]) {
+  ChunkScanArgs p;
+  p.x = x;
+  p.sxb = x_strides[0];
+  p.sxl = x_strides[1];
+  p.sxh = x_strides[2];
+  p.bm = bmat;
+  p.sbb = b_strides[0];
+  p.sbl = b_strides[1];
+  p.sbg = b_strides[2];
+  p.cm = cmat;
+  p.scb = c_strides[0];
+  p.scl = c_strides[1];
+  p.scg = c_strides[2];
+  p.dt = dt;
+  p.sdb = dt ? dt_strides[0] : 0;
+  p.sdl = dt ? dt_strides[1] : 0;
+  p.sdh = dt ? dt_strides[2] : 0;
+  p.acs = a_cumsum;
+  p.states = states;
+  p.y = y;
+  p.syb = y_strides[0];
+  p.syl = y_strides[1];
+  p.syh = y_strides[2];
+  p.batch = (int)d->batch;
+  p.nchunks = (int)(d->seqlen / d->chunk);
+  p.nheads = (int)d->nheads;
+  p.ngroups = (int)d->ngroups;
+  p.dstate = (int)d->dstate;
+  p.chunk = (int)d->chunk;
+  return p;
 }
 
 }  // namespace
@@ -180,10 +313,29 @@ int ssd_chunk_cumsum(const ssd_dims* d, const float* a, const int64_t a_strides[
   return hip_status(ssd::launch_chunk_cumsum(p, (hipStream_t)stream));
 }
 
+size_t ssd_chunk_prep_bytes(const ssd_dims* d) {
+  if (check_dims_impl(d, SSD_DTYPE_BF16) != SSD_OK) return 0;
+  return prep_bytes(d);
+}
+
+int ssd_chunk_prep(const ssd_dims* d, int dtype, const void* bmat, const int64_t b_strides[4], const void* cmat,
+                   const int64_t c_strides[4], void* prep, size_t prep_bytes_given, void* stream) {
+  int rc = check_dims_impl(d, dtype);
+  if (rc) return rc;
+  if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
+  if ((rc = check_vec_operand(cmat, c_strides, 4, dtype))) return rc;
+  if (!prep_applies(d, dtype)) return SSD_OK;
+  if (!prep) return SSD_ERR_NULL_POINTER;
+  if ((reinterpret_cast<uintptr_t>(prep) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
+  if (prep_bytes_given < prep_bytes(d)) return SSD_ERR_WORKSPACE_TOO_SMALL;
+  return hip_status(ssd::launch_chunk_prep(make_prep_args(d, bmat, b_strides, cmat, c_strides, prep), dtype,
+                                           (hipStream_t)stream));
+}
+
 int ssd_chunk_state(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4],
                     const void* bmat, const int64_t b_strides[4], const float* dt,
                     const int64_t dt_strides[3], const float* a_cumsum, void* states,
-                    int state_dtype, void* stream) {
+                    int state_dtype, const void* prep, void* stream) {
   int rc = check_dims_impl(d, dtype);
   if (rc) return rc;
   if (!valid_state_dtype(dtype, state_dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
@@ -192,27 +344,9 @@ int ssd_chunk_state(const ssd_dims* d, int dtype, const void* x, const int64_t x
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
   if (!a_cumsum || !states) return SSD_ERR_NULL_POINTER;
   if (!aligned16(states)) return SSD_ERR_MISALIGNED;
-  ChunkStateArgs p;
-  p.x = x;
-  p.sxb = x_strides[0];
-  p.sxl = x_strides[1];
-  p.sxh = x_strides[2];
-  p.bm = bmat;
-  p.sbb = b_strides[0];
-  p.sbl = b_strides[1];
-  p.sbg = b_strides[2];
-  p.dt = dt;
-  p.sdb = dt ? dt_strides[0] : 0;
-  p.sdl = dt ? dt_strides[1] : 0;
-  p.sdh = dt ? dt_strides[2] : 0;
-  p.acs = a_cumsum;
-  p.states = states;
-  p.batch = (int)d->batch;
-  p.nchunks = (int)(d->seqlen / d->chunk);
-  p.nheads = (int)d->nheads;
-  p.ngroups = (int)d->ngroups;
-  p.dstate = (int)d->dstate;
-  p.chunk = (int)d->chunk;
+  if (prep && (reinterpret_cast<uintptr_t>(prep) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
+  ChunkStateArgs p = make_state_args(d, x, x_strides, bmat, b_strides, dt, dt_strides, a_cumsum, states);
+  if (prep_applies(d, dtype)) p.btf = prep_btf(d, prep);
   return hip_status(ssd::launch_chunk_state(p, dtype, state_dtype, (hipStream_t)stream));
 }
 
@@ -220,68 +354,42 @@ int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, const fl
                       const float* initial_states, float* final_states, void* stream) {
   int rc = check_dims_impl(d, SSD_DTYPE_BF16);
   if (rc) return rc;
-  if (state_dtype != SSD_DTYPE_F32 && state_dtype != SSD_DTYPE_BF16) return SSD_ERR_UNSUPPORTED_DTYPE;
+  const int split = split_of(state_dtype);
+  if (state_dtype != SSD_DTYPE_F32 && state_dtype != SSD_DTYPE_BF16 && !split) return SSD_ERR_UNSUPPORTED_DTYPE;
   if (!states || !chunk_decay) return SSD_ERR_NULL_POINTER;
   if (!aligned16(states) || (initial_states && !aligned16(initial_states)) ||
       (final_states && !aligned16(final_states)))
     return SSD_ERR_MISALIGNED;
-  StatePassingArgs p;
-  p.states = states;
-  p.decay = chunk_decay;
-  p.init = initial_states;
-  p.final_state = final_states;
-  p.batch = (int)d->batch;
-  p.nchunks = (int)(d->seqlen / d->chunk);
-  p.nheads = (int)d->nheads;
-  p.headdim = (int)d->headdim;
-  p.dstate = (int)d->dstate;
-  return hip_status(ssd::launch_state_passing(p, state_dtype, (hipStream_t)stream));
+  StatePassingArgs p = make_sp_args(d, states, chunk_decay, initial_states, final_states);
+  p.split_dtype = split;
+  return hip_status(ssd::launch_state_passing(p, split ? SSD_DTYPE_F32 : state_dtype, (hipStream_t)stream));
 }
 
 int ssd_chunk_scan(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4],
                    const void* bmat, const int64_t b_strides[4], const void* cmat,
                    const int64_t c_strides[4], const float* dt, const int64_t dt_strides[3],
                    const float* a_cumsum, const void* states, int state_dtype, void* y,
-                   const int64_t y_strides[4], void* stream) {
+                   const int64_t y_strides[4], const void* prep, void* stream) {
   int rc = check_dims_impl(d, dtype);
   if (rc) return rc;
-  if (!valid_state_dtype(dtype, state_dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+  const int split = split_of(state_dtype);
+  if (!valid_state_dtype(dtype, state_dtype) && !(split && split == dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
   if ((rc = check_vec_operand(x, x_strides, 4, dtype))) return rc;
   if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
   if ((rc = check_vec_operand(cmat, c_strides, 4, dtype))) return rc;
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
   if (!a_cumsum || !states) return SSD_ERR_NULL_POINTER;
   if ((rc = check_output(y, y_strides, dtype))) return rc;
-  ChunkScanArgs p;
-  p.x = x;
-  p.sxb = x_strides[0];
-  p.sxl = x_strides[1];
-  p.sxh = x_strides[2];
-  p.bm = bmat;
-  p.sbb = b_strides[0];
-  p.sbl = b_strides[1];
-  p.sbg = b_strides[2];
-  p.cm = cmat;
-  p.scb = c_strides[0];
-  p.scl = c_strides[1];
-  p.scg = c_strides[2];
-  p.dt = dt;
-  p.sdb = dt ? dt_strides[0] : 0;
-  p.sdl = dt ? dt_strides[1] : 0;
-  p.sdh = dt ? dt_strides[2] : 0;
-  p.acs = a_cumsum;
-  p.states = states;
-  p.y = y;
-  p.syb = y_strides[0];
-  p.syl = y_strides[1];
-  p.syh = y_strides[2];
-  p.batch = (int)d->batch;
-  p.nchunks = (int)(d->seqlen / d->chunk);
-  p.nheads = (int)d->nheads;
-  p.ngroups = (int)d->ngroups;
-  p.dstate = (int)d->dstate;
-  p.chunk = (int)d->chunk;
-  return hip_status(ssd::launch_chunk_scan(p, dtype, state_dtype, (hipStream_t)stream));
+  if (prep && (reinterpret_cast<uintptr_t>(prep) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
+  ChunkScanArgs p = make_scan_args(d, x, x_strides, bmat, b_strides, cmat, c_strides, dt, dt_strides, a_cumsum,
+                                   states, y, y_strides);
+  if (prep_applies(d, dtype)) p.cbf = prep_cbf(prep);
+  if (split) {
+    // only the chunk-256 kernel reads split states
+    if (!prep_applies(d, dtype) || !ssd::chunk_scan_persistent_supported(p, dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+    p.presplit = true;
+  }
+  return hip_status(ssd::launch_chunk_scan(p, dtype, split ? SSD_DTYPE_F32 : state_dtype, (hipStream_t)stream));
 }
 
 int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4], const float* a,
@@ -312,13 +420,28 @@ int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_str
   float* acs = reinterpret_cast<float*>(ws + w.acs);
   float* decay = reinterpret_cast<float*>(ws + w.decay);
   void* states = ws + w.states;
+  ChunkStateArgs sa = make_state_args(d, x, x_strides, bmat, b_strides, dt, dt_strides, acs, states);
+  ChunkScanArgs ca = make_scan_args(d, x, x_strides, bmat, b_strides, cmat, c_strides, dt, dt_strides, acs, states,
+                                    y, y_strides);
+  const hipStream_t s = (hipStream_t)stream;
   if ((rc = ssd_chunk_cumsum(d, a, a_strides, acs, decay, stream))) return rc;
-  if ((rc = ssd_chunk_state(d, dtype, x, x_strides, bmat, b_strides, dt, dt_strides, acs, states,
-                            state_dtype, stream)))
-    return rc;
-  if ((rc = ssd_state_passing(d, states, state_dtype, decay, initial_states, final_states, stream))) return rc;
-  return ssd_chunk_scan(d, dtype, x, x_strides, bmat, b_strides, cmat, c_strides, dt, dt_strides, acs, states,
-                        state_dtype, y, y_strides, stream);
+  // K0: the persistent kernels' per-group operands, once per (b, c, group)
+  if (prep_applies(d, dtype)) {
+    void* prep = ws + w.prep;
+    if ((rc = hip_status(ssd::launch_chunk_prep(make_prep_args(d, bmat, b_strides, cmat, c_strides, prep), dtype, s))))
+      return rc;
+    sa.btf = prep_btf(d, prep);
+    ca.cbf = prep_cbf(prep);
+  }
+  if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, state_dtype, s)))) return rc;
+  // f32 states for the chunk-256 chunk_scan: K3 writes them as its hi/lo operand pairs
+  StatePassingArgs pa = make_sp_args(d, states, decay, initial_states, final_states);
+  if (state_dtype == SSD_DTYPE_F32 && prep_applies(d, dtype) && ssd::chunk_scan_persistent_supported(ca, dtype)) {
+    pa.split_dtype = dtype;
+    ca.presplit = true;
+  }
+  if ((rc = hip_status(ssd::launch_state_passing(pa, state_dtype, s)))) return rc;
+  return hip_status(ssd::launch_chunk_scan(ca, dtype, state_dtype, s));
 }
 
 }  // extern "C"

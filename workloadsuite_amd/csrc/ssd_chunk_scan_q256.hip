@@ -73,6 +73,8 @@ struct ScanArgs32 {
   const float* acs;
   const void* states;
   void* y;
+  const float* cbf;  // chunk_prep's CB^T fragments, or null
+  int presplit;      // f32 S_in already stored as [hi x8 | lo x8] pairs
   int sxb, sxl, sxh, sbb, sbl, sbg, scb, scl, scg, sdb, sdl, sdh, syb, syl, syh;
   int batch, nchunks, nheads, ngroups, dstate;
 };
@@ -91,7 +93,7 @@ __device__ __forceinline__ Item item_of(const ScanArgs32& p, int it) {
   return r;
 }
 
-template <typename T, typename S, int NK, bool HAS_DT>
+template <typename T, typename S, int NK, bool HAS_DT, bool PREP>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void chunk_scan_q256_kernel(ScanArgs32 p) {
   constexpr int N = 32 * NK;                      // dstate (64 or 128)
@@ -120,8 +122,10 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   __builtin_assume(wave < kNW);  // lets the tile-range tests below fold
   const int g = lane >> 4, i = lane & 15;
   const int nitems = p.batch * p.nchunks * p.nheads;
-  const int it0 = (int)((int64_t)blockIdx.x * nitems / gridDim.x);
-  const int it1 = (int)((int64_t)(blockIdx.x + 1) * nitems / gridDim.x);
+  // consecutive item ranges (which share B and C) go to one XCD's L2
+  const int lb = xcd_remap(blockIdx.x, gridDim.x);
+  const int it0 = (int)((int64_t)lb * nitems / gridDim.x);
+  const int it1 = (int)((int64_t)(lb + 1) * nitems / gridDim.x);
   if (it0 >= it1) return;
   const int ta = wave, tb = kNT - 1 - wave;
   const int KA = ta / 2 + 1;  // s blocks of tile ta; tile tb has the other kNPair - KA
@@ -220,7 +224,8 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     __syncthreads();  // every G read its block's unscaled last Acs
     for (int e = tid; e < kQ; e += kThreads) ar[b][e] *= kLog2e;
     if constexpr (SPLIT) {
-      for (int u = tid; u < kP * (N / 8); u += kThreads) {
+      // (with presplit the copy already holds the pairs)
+      for (int u = p.presplit ? kP * (N / 8) : tid; u < kP * (N / 8); u += kThreads) {
         // pair q = pieces 2q, 2q+1 (8 states) -> hi at piece 2q's slot, lo at 2q+1's
         const int row = u / (N / 8), q = u % (N / 8), sw = ssw(row);
         unsigned char* ph = sr[b] + row * RB + 16 * ((2 * q) ^ sw);
@@ -265,6 +270,16 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     for (int kc = 0; kc < NK; ++kc) {
       cf[0][kc] = load8<T>(cg + (int64_t)(16 * ta + i) * p.scl + 32 * kc + 8 * g);
       cf[1][kc] = load8<T>(cg + (int64_t)(16 * tb + i) * p.scl + 32 * kc + 8 * g);
+    }
+    if constexpr (PREP) {
+      // precomputed by chunk_prep in this order: one round of independent loads
+      const f32x4* cb = reinterpret_cast<const f32x4*>(p.cbf) +
+                        ((((int64_t)r.b * p.nchunks + r.c) * p.ngroups + r.grp) * kNW + wave) * (kNPair * 2 * 64) + lane_o;
+#pragma unroll
+      for (int k = 0; k < kNPair; ++k)
+#pragma unroll
+        for (int st = 0; st < 2; ++st) cbc[k][st] = cb[(k * 2 + st) * 64];
+      return;
     }
     // One 32-token s block (two 16x16 sub-tiles) per step; every row lies in
     // the chunk, so all loads of a step issue together, and a sub-tile
@@ -464,7 +479,12 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     prev = cur;
     if (has_next) {
       convert(bn);
-      if (nxt.b != cur.b || nxt.c != cur.c || nxt.grp != cur.grp) load_group(it + 1);
+      if (nxt.b != cur.b || nxt.c != cur.c || nxt.grp != cur.grp) {
+        load_group(it + 1);
+        // complete before the next item's copies are issued: the compiler's
+        // wait before the first use would also count those copies
+        dma_wait();
+      }
       cur = nxt;
     }
     __syncthreads();
@@ -484,6 +504,8 @@ ScanArgs32 narrow(const ChunkScanArgs& a) {
   n.acs = a.acs;
   n.states = a.states;
   n.y = a.y;
+  n.cbf = a.cbf;
+  n.presplit = a.presplit ? 1 : 0;
   n.sxb = (int)a.sxb, n.sxl = (int)a.sxl, n.sxh = (int)a.sxh;
   n.sbb = (int)a.sbb, n.sbl = (int)a.sbl, n.sbg = (int)a.sbg;
   n.scb = (int)a.scb, n.scl = (int)a.scl, n.scg = (int)a.scg;
@@ -495,7 +517,8 @@ ScanArgs32 narrow(const ChunkScanArgs& a) {
 
 template <typename T, typename S, int NK>
 hipError_t launch_nk(const ChunkScanArgs& a, hipStream_t stream) {
-  auto kern = a.dt ? chunk_scan_q256_kernel<T, S, NK, true> : chunk_scan_q256_kernel<T, S, NK, false>;
+  auto kern = a.dt ? (a.cbf ? chunk_scan_q256_kernel<T, S, NK, true, true> : chunk_scan_q256_kernel<T, S, NK, true, false>)
+                   : (a.cbf ? chunk_scan_q256_kernel<T, S, NK, false, true> : chunk_scan_q256_kernel<T, S, NK, false, false>);
   const int items = a.batch * a.nchunks * a.nheads;
   const int grid = persistent_grid(kern, kThreads, items);
   kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(narrow(a));

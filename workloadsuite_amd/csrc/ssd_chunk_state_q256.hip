@@ -65,11 +65,8 @@ template <> struct StateStore<bf16> {
   }
 };
 
-// K slot j of lane group g stands for token 4 g + j (j < 4) or 16 + 4 g + j - 4
-// (j >= 4) of a 32-token step: the rows a pair of transposing reads delivers.
-__device__ __forceinline__ int slot_token(int g, int j) { return (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4)); }
 
-template <typename T, typename S, int NK, bool HAS_DT>
+template <typename T, typename S, int NK, bool HAS_DT, bool PREP>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void chunk_state_q256_kernel(ChunkStateArgs p) {
   constexpr int N = 32 * NK;        // dstate (64 or 128)
@@ -84,8 +81,10 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
   __builtin_assume(wave < kNW);
   const int g = lane >> 4, i = lane & 15;
   const int nitems = p.batch * p.nchunks * p.nheads;
-  const int it0 = (int)((int64_t)blockIdx.x * nitems / gridDim.x);
-  const int it1 = (int)((int64_t)(blockIdx.x + 1) * nitems / gridDim.x);
+  // consecutive item ranges (which share B and C) go to one XCD's L2
+  const int lb = xcd_remap(blockIdx.x, gridDim.x);
+  const int it0 = (int)((int64_t)lb * nitems / gridDim.x);
+  const int it1 = (int)((int64_t)(lb + 1) * nitems / gridDim.x);
   if (it0 >= it1) return;
   const int nt = wave % NTILE, pt0 = (wave / NTILE) * PTW;  // this wave's n tile and first p tile
 
@@ -141,6 +140,14 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
     asm volatile("" : "+v"(lane_o));  // opaque: per-group address math, not hoisted
     const int go = lane_o >> 4, io = lane_o & 15;
     const Item r = item_of(p, it);
+    if constexpr (PREP) {
+      // chunk_prep's fragments: one 16-byte load per K step
+      const frag8<T>* bf = reinterpret_cast<const frag8<T>*>(p.btf) +
+                           ((((int64_t)r.b * p.nchunks + r.c) * p.ngroups + r.grp) * NTILE + nt) * (kKS * 64) + lane_o;
+#pragma unroll
+      for (int ks = 0; ks < kKS; ++ks) bt[ks] = bf[ks * 64];
+      return;
+    }
     const int64_t l0 = (int64_t)r.c * kQ;
     const T* bg = reinterpret_cast<const T*>(p.bm) + r.b * p.sbb + l0 * p.sbl + r.grp * p.sbg + 16 * nt + io;
 #pragma unroll
@@ -205,7 +212,12 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
     if (has_next) {
       tabulate(bn);
       const Item nxt = item_of(p, it + 1);
-      if (nxt.b != cur.b || nxt.c != cur.c || nxt.grp != cur.grp) load_group(it + 1);
+      if (nxt.b != cur.b || nxt.c != cur.c || nxt.grp != cur.grp) {
+        load_group(it + 1);
+        // complete before the next item's copies are issued: the compiler's
+        // wait before the first use would also count those copies
+        dma_wait();
+      }
       cur = nxt;
     }
     __syncthreads();
@@ -215,7 +227,8 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
 
 template <typename T, typename S, int NK>
 hipError_t launch_nk(const ChunkStateArgs& a, hipStream_t stream) {
-  auto kern = a.dt ? chunk_state_q256_kernel<T, S, NK, true> : chunk_state_q256_kernel<T, S, NK, false>;
+  auto kern = a.dt ? (a.btf ? chunk_state_q256_kernel<T, S, NK, true, true> : chunk_state_q256_kernel<T, S, NK, true, false>)
+                   : (a.btf ? chunk_state_q256_kernel<T, S, NK, false, true> : chunk_state_q256_kernel<T, S, NK, false, false>);
   const int items = a.batch * a.nchunks * a.nheads;
   const int grid = persistent_grid(kern, kThreads, items);
   kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(a);

@@ -191,6 +191,10 @@ __device__ __forceinline__ void dma4(const void* g, void* lds_base) { dma4_at(g,
 // s_waitcnt vmcnt(0): every vector memory operation of this wave has completed.
 __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
 
+// MFMA K slot j of lane group g stands for token 4 g + j (j < 4) or 16 + 4 g + j - 4
+// (j >= 4) of a 32-token step: the rows a pair of transposing reads delivers.
+__device__ __forceinline__ int slot_token(int g, int j) { return (j < 4 ? 4 * g + j : 16 + 4 * g + (j - 4)); }
+
 // ---------------------------------------------------------------------------
 // Workgroup -> tile mapping.  Hardware dispatches workgroup ids round-robin
 // over the 8 XCDs (id % 8), each with its own L2.  The remap hands every XCD a

@@ -27,6 +27,7 @@ struct ChunkStateArgs {
   const float* acs;       // [b, h, c, Q]
   void* states;           // [b, c, h, P, N]
   int batch, nchunks, nheads, ngroups, dstate, chunk;
+  const void* btf = nullptr;  // optional chunk_prep B^T fragments (persistent kernel)
 };
 
 struct StatePassingArgs {
@@ -35,6 +36,9 @@ struct StatePassingArgs {
   const float* init;      // optional [b, h, P, N]
   float* final_state;     // optional [b, h, P, N]
   int batch, nchunks, nheads, headdim, dstate;
+  // 0, or SSD_DTYPE_BF16 / F16: f32 S_in is written as chunk_scan's hi/lo
+  // operand pairs of that type (chunk-256 forward path only)
+  int split_dtype = 0;
 };
 
 struct ChunkScanArgs {
@@ -51,7 +55,24 @@ struct ChunkScanArgs {
   void* y;
   int64_t syb, syl, syh;  // y [b, L, h, P], unit stride over P
   int batch, nchunks, nheads, ngroups, dstate, chunk;
+  const float* cbf = nullptr;  // optional chunk_prep CB^T fragments (persistent kernel)
+  bool presplit = false;       // f32 states already split by state_passing (split_dtype)
 };
+
+// K0 -- per-(b, c, group) operands of the chunk-256 persistent kernels
+// (ssd_chunk_prep.hip): CB^T blocks for chunk_scan, B^T fragments for chunk_state.
+struct ChunkPrepArgs {
+  const void* bm;
+  int64_t sbb, sbl, sbg;
+  const void* cm;
+  int64_t scb, scl, scg;
+  int batch, nchunks, ngroups, dstate, chunk;
+  float* cbf;  // chunk_prep_cb_bytes(batch * nchunks * ngroups)
+  void* btf;   // chunk_prep_bt_bytes(batch * nchunks * ngroups, dstate)
+};
+size_t chunk_prep_cb_bytes(int64_t groups);
+size_t chunk_prep_bt_bytes(int64_t groups, int dstate);
+hipError_t launch_chunk_prep(const ChunkPrepArgs& a, int dtype, hipStream_t stream);
 
 // Compute units of the current device (cached per device id after the first
 // query; 0 when the query fails).

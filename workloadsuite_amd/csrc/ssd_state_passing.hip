@@ -79,10 +79,81 @@ __global__ __launch_bounds__(256) void state_passing_kernel(StatePassingArgs p) 
   if (p.final_state) *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * PN + 4 * (int64_t)v) = st;
 }
 
+// f32 states handed to the chunk-256 chunk_scan: S_in is written as that
+// kernel's MFMA operands -- every 8 consecutive states (32 bytes) become
+// [hi x8 | lo x8] of T, hi = T(v), lo = T(v - hi) -- so chunk_scan does not
+// split it again per item.  The recurrence and final_state stay f32.
+// Thread mapping as in state_passing_kernel (4 states, one 16-byte load per
+// chunk); lane pairs then swap halves so that the even lane stores the 8 hi
+// and the odd lane the 8 lo values of their 8 states: 16 contiguous bytes per
+// lane, 1 KB per wave store.
+template <typename T>
+__global__ __launch_bounds__(256) void state_passing_split_kernel(StatePassingArgs p) {
+  const int64_t PN = (int64_t)p.headdim * p.dstate;
+  const int vec_per_bh = (int)(PN / 4);
+  const int blocks_per_bh = (vec_per_bh + 255) / 256;
+  const int bh = blockIdx.x / blocks_per_bh;
+  const int v = (blockIdx.x % blocks_per_bh) * 256 + threadIdx.x;
+  if (v >= vec_per_bh) return;  // vec_per_bh is a multiple of 256: whole waves leave together
+  const int h = bh % p.nheads, b = bh / p.nheads;
+  const bool odd = threadIdx.x & 1;
+
+  float* base = reinterpret_cast<float*>(p.states) + ((int64_t)b * p.nchunks * p.nheads + h) * PN + 4 * (int64_t)v;
+  const int64_t cstride = (int64_t)p.nheads * PN;
+  const float* dec = p.decay + (int64_t)bh * p.nchunks;
+
+  f32x4 st = p.init ? *reinterpret_cast<const f32x4*>(p.init + (int64_t)bh * PN + 4 * (int64_t)v)
+                    : f32x4{0.f, 0.f, 0.f, 0.f};
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  for (int c0 = 0; c0 < p.nchunks; c0 += kUnroll) {
+    f32x4 loc[kUnroll];
+    float d[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (c0 + u < p.nchunks) {
+        loc[u] = *reinterpret_cast<const f32x4*>(base + (c0 + u) * cstride);
+        d[u] = dec[c0 + u];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (c0 + u < p.nchunks) {
+        vec4<T> hi, lo;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          hi[k] = from_f32<T>(st[k]);
+          lo[k] = from_f32<T>(st[k] - to_f32<T>(hi[k]));
+        }
+        const u32x2 hw = __builtin_bit_cast(u32x2, hi), lw = __builtin_bit_cast(u32x2, lo);
+        // even lane keeps its hi and receives the odd lane's hi; odd lane the reverse for lo
+        const u32x2 give = odd ? hw : lw, keep = odd ? lw : hw;
+        u32x2 got;
+        got[0] = (uint32_t)__builtin_amdgcn_mov_dpp((int)give[0], 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+        got[1] = (uint32_t)__builtin_amdgcn_mov_dpp((int)give[1], 0xB1, 0xF, 0xF, false);
+        const u32x4 out = odd ? u32x4{got[0], got[1], keep[0], keep[1]} : u32x4{keep[0], keep[1], got[0], got[1]};
+        // the pair's 32 bytes start at the even lane's 16: hi at +0, lo at +16
+        *reinterpret_cast<u32x4*>(base + (c0 + u) * cstride) = out;
+        st = st * d[u] + loc[u];
+      }
+    }
+  }
+  if (p.final_state) *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * PN + 4 * (int64_t)v) = st;
+}
+
 }  // namespace
 
 hipError_t launch_state_passing(const StatePassingArgs& a, int state_dtype, hipStream_t stream) {
   const int64_t PN = (int64_t)a.headdim * a.dstate;
+  if (a.split_dtype != 0) {
+    if (state_dtype != SSD_DTYPE_F32 || PN % 8 != 0) return hipErrorInvalidValue;
+    if (PN % 256 != 0) return hipErrorInvalidValue;  // whole waves per (b, h)
+    const dim3 grid((unsigned)((int64_t)a.batch * a.nheads * ((PN / 4 + 255) / 256)));
+    if (a.split_dtype == SSD_DTYPE_BF16) state_passing_split_kernel<bf16><<<grid, 256, 0, stream>>>(a);
+    else if (a.split_dtype == SSD_DTYPE_F16) state_passing_split_kernel<f16><<<grid, 256, 0, stream>>>(a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   const int64_t blocks_per_bh = (PN / 4 + 255) / 256;
   const dim3 grid((unsigned)((int64_t)a.batch * a.nheads * blocks_per_bh));
   if (state_dtype == SSD_DTYPE_F32) {

@@ -19,7 +19,7 @@ and its error behaviour: a seqlen that is not a multiple of the chunk size
 ``ValueError``) raise ``ValueError`` here too.  Like MR, the op is pure: it
 allocates fresh outputs and never mutates its inputs.
 
-All arithmetic runs in libssd.so's four HIP kernels on the tensors' device
+All arithmetic runs in libssd.so's HIP kernels on the tensors' device
 and on torch's current stream.  There is no CPU path: tensors on another
 device, or a missing library, raise.  The op is forward-only (no autograd),
 as the reference harness runs it under ``torch.inference_mode()``.
@@ -37,6 +37,7 @@ __all__ = [
     "ssd_forward",
     "ssd_core",
     "chunk_cumsum",
+    "chunk_prep",
     "chunk_state",
     "state_passing",
     "state_passing_",
@@ -49,6 +50,8 @@ SSDError = _lib.SSDError
 
 _DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
 _STATE_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
+# f32 states stored as 16-bit (hi, lo) pairs of the inputs' type
+_SPLIT_STATES = {torch.bfloat16: _lib.STATE_SPLIT_BF16, torch.float16: _lib.STATE_SPLIT_F16}
 
 
 def _device_check(*ts):
@@ -216,8 +219,31 @@ def chunk_cumsum(A, chunk_size):
     return Acs, decay
 
 
-def chunk_state(X, B, Acs, dt=None, state_dtype=torch.float32):
-    """K2: local states [b, c, h, P, N] (MR:144, 148-149)."""
+def chunk_prep(B, C, chunk_size):
+    """K0: the chunk-256 kernels' per-(batch, chunk, group) operands -- C.B^T
+    (MR:143) and B in their register order -- as an opaque uint8 buffer for
+    ``chunk_state`` / ``chunk_scan`` (``prep=``), or None for shapes and dtypes
+    without that path (the kernels then rebuild them themselves)."""
+    b, L, g, N = B.shape
+    if C.shape != B.shape:
+        raise ValueError("B and C must have the same shape [batch, seqlen, ngroups, dstate]")
+    dev = _device_check(B, C)
+    if chunk_size < 1 or L % chunk_size != 0:
+        raise ValueError(f"seqlen {L} is not a multiple of chunk size {chunk_size}")
+    lib = _lib.load()
+    d = _dims(b, L, g, 64, N, g, chunk_size)
+    n = lib.ssd_chunk_prep_bytes(ctypes.byref(d))
+    if n == 0 or B.dtype == torch.float32:
+        return None
+    Bm, Cm = _vec_operand(B.detach()), _vec_operand(C.detach())
+    prep = torch.empty(n, dtype=torch.uint8, device=dev)
+    _lib.check(lib.ssd_chunk_prep(ctypes.byref(d), _DTYPES[Bm.dtype], _ptr(Bm), _lib.strides(Bm), _ptr(Cm),
+                                  _lib.strides(Cm), _ptr(prep), n, _stream(dev)))
+    return prep
+
+
+def chunk_state(X, B, Acs, dt=None, state_dtype=torch.float32, prep=None):
+    """K2: local states [b, c, h, P, N] (MR:144, 148-149).  ``prep``: chunk_prep(B, C, Q) or None."""
     b, L, h, P = X.shape
     g, N = B.shape[2], B.shape[3]
     Q = Acs.shape[-1]
@@ -230,23 +256,25 @@ def chunk_state(X, B, Acs, dt=None, state_dtype=torch.float32):
     _lib.check(_lib.load().ssd_chunk_state(
         ctypes.byref(d), _DTYPES[X.dtype], _ptr(X), _lib.strides(X), _ptr(Bm), _lib.strides(Bm),
         _ptr(dt), _lib.strides(dt) if dt is not None else None, _ptr(Acs), _ptr(states),
-        _STATE_DTYPES[state_dtype], _stream(dev)))
+        _STATE_DTYPES[state_dtype], _ptr(prep), _stream(dev)))
     return states
 
 
-def state_passing(states, chunk_decay, initial_states=None, return_final_states=True):
+def state_passing(states, chunk_decay, initial_states=None, return_final_states=True, split=None):
     """K3: (S_in [b, c, h, P, N], final [b, h, P, N]) from local states (MR:152-157).
 
-    Works on a copy: the input ``states`` is left unchanged.
+    Works on a copy: the input ``states`` is left unchanged.  ``split``
+    (torch.bfloat16 / torch.float16, f32 states only): S_in is stored as that
+    type's (hi, lo) pairs for ``chunk_scan(..., split=True)``.
     """
     S = states.detach().clone(memory_format=torch.contiguous_format)
     final = (torch.empty((S.shape[0], S.shape[2], S.shape[3], S.shape[4]), dtype=torch.float32, device=S.device)
              if return_final_states else None)
-    state_passing_(S, chunk_decay, initial_states, final)
+    state_passing_(S, chunk_decay, initial_states, final, split=split)
     return S, final
 
 
-def state_passing_(states, chunk_decay, initial_states=None, final_states=None):
+def state_passing_(states, chunk_decay, initial_states=None, final_states=None, split=None):
     """K3 in place on a contiguous ``states`` buffer (local states in, S_in out);
     ``final_states`` (optional, [b, h, P, N] float32) receives the last state."""
     b, nc, h, P, N = states.shape
@@ -259,13 +287,18 @@ def state_passing_(states, chunk_decay, initial_states=None, final_states=None):
     if final_states is not None and (final_states.dtype != torch.float32 or not final_states.is_contiguous()
                                      or final_states.shape != (b, h, P, N)):
         raise ValueError("final_states must be a contiguous float32 [b, h, P, N] tensor")
-    _lib.check(_lib.load().ssd_state_passing(ctypes.byref(d), _ptr(states), _STATE_DTYPES[states.dtype],
+    if split is not None and (states.dtype != torch.float32 or split not in _SPLIT_STATES):
+        raise ValueError("split storage needs float32 states and split=torch.bfloat16 or torch.float16")
+    sd = _STATE_DTYPES[states.dtype] if split is None else _SPLIT_STATES[split]
+    _lib.check(_lib.load().ssd_state_passing(ctypes.byref(d), _ptr(states), sd,
                                              _ptr(decay), _ptr(init), _ptr(final_states), _stream(dev)))
     return states
 
 
-def chunk_scan(X, B, C, Acs, states, dt=None):
-    """K4: Y [b, L, h, P] from the states entering each chunk (MR:139-145, 160-162)."""
+def chunk_scan(X, B, C, Acs, states, dt=None, prep=None, split=False):
+    """K4: Y [b, L, h, P] from the states entering each chunk (MR:139-145, 160-162).
+    ``prep``: chunk_prep(B, C, Q) or None.  ``split``: ``states`` holds
+    state_passing(..., split=X.dtype)'s (hi, lo) pairs."""
     b, L, h, P = X.shape
     g, N = B.shape[2], B.shape[3]
     Q = Acs.shape[-1]
@@ -281,5 +314,6 @@ def chunk_scan(X, B, C, Acs, states, dt=None):
     _lib.check(_lib.load().ssd_chunk_scan(
         ctypes.byref(d), _DTYPES[X.dtype], _ptr(X), _lib.strides(X), _ptr(Bm), _lib.strides(Bm),
         _ptr(Cm), _lib.strides(Cm), _ptr(dt), _lib.strides(dt) if dt is not None else None,
-        _ptr(Acs), _ptr(S), _STATE_DTYPES[S.dtype], _ptr(Y), _lib.strides(Y), _stream(dev)))
+        _ptr(Acs), _ptr(S), _SPLIT_STATES[X.dtype] if split else _STATE_DTYPES[S.dtype], _ptr(Y),
+        _lib.strides(Y), _ptr(prep), _stream(dev)))
     return Y
