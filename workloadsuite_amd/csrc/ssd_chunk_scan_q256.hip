@@ -337,6 +337,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     // off-diagonal: acc[s2][pt] = S_in[p, :] . C[l, :], then * exp(Acs[l])
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) {
+      set_prio(3);  // waves behind in the item go first
       off_step(pt);
 #pragma unroll
       for (int kc = 0; kc < NK; ++kc) {
@@ -397,6 +398,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     // diagonal, step j: s block j of tile ta (j < KA) and of tile tb (j < KB)
 #pragma unroll
     for (int j = 0; j < kNPair - 1; ++j) {
+      set_prio(2 - (j + 1) / 3);
       const bool do_a = j < KA, do_b = j < KB;  // wave-uniform
       if (!do_b) continue;                       // KB >= KA: nothing left for either tile
       f32x4 gs[2];

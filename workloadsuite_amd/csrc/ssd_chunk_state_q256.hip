@@ -35,8 +35,9 @@ namespace {
 
 constexpr int kP = 64;
 constexpr int kQ = 256;
-constexpr int kNW = 8;               // waves per workgroup
-constexpr int kThreads = 64 * kNW;
+constexpr int kNW = 8;               // waves per half workgroup
+constexpr int kHalves = 2;           // two items in flight per workgroup
+constexpr int kThreads = 64 * kNW * kHalves;
 constexpr int kKS = kQ / 32;         // 32-token K steps
 constexpr int kXBlocks = kQ / 8;     // 1 KB copy blocks of x (8 rows of 64 x 16-bit)
 
@@ -72,12 +73,15 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
   constexpr int N = 32 * NK;        // dstate (64 or 128)
   constexpr int NTILE = N / 16;     // n tiles
   constexpr int PTW = NTILE / 2;    // p tiles per wave (4 for N=128, 2 for N=64)
-  __shared__ __attribute__((aligned(1024))) T xr[2][kQ * kP];
-  __shared__ __attribute__((aligned(16))) float ar[2][kQ];
-  __shared__ __attribute__((aligned(16))) float dr[HAS_DT ? 2 : 1][HAS_DT ? kQ : 4];
-  __shared__ __attribute__((aligned(16))) float wr[kQ];  // w[l] of the current item
+  // [half][buffer]: each half's current item and its next one (in flight)
+  __shared__ __attribute__((aligned(1024))) T xr[kHalves][2][kQ * kP];
+  __shared__ __attribute__((aligned(16))) float ar[kHalves][2][kQ];
+  __shared__ __attribute__((aligned(16))) float dr[kHalves][HAS_DT ? 2 : 1][HAS_DT ? kQ : 4];
+  __shared__ __attribute__((aligned(16))) float wr[kHalves][kQ];  // w[l] of each half's current item
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, htid = tid & 511, lane = tid & 63;
+  const int half = __builtin_amdgcn_readfirstlane(tid >> 9);        // wave-uniform
+  const int wave = __builtin_amdgcn_readfirstlane((tid >> 6) & 7);  // wave within the half
   __builtin_assume(wave < kNW);
   const int g = lane >> 4, i = lane & 15;
   const int nitems = p.batch * p.nchunks * p.nheads;
@@ -103,43 +107,50 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
   // states [p][n]: row 16 pt + i, columns 16 nt + 4 g .. + 3
   const int srow = (16 * pt0 + i) * N + 16 * nt + 4 * g;
 
-  auto issue_copy = [&](int it, int b) __attribute__((always_inline)) {
-    const Item r = item_of(p, it);
+  // Part m (0..3) of one item's copy into this half's buffer b: x block
+  // wave + 8 m; part 0 also Acs (and dt).  Parts are issued between compute
+  // steps, so a wave's vector memory queue never holds up its MFMAs for a
+  // whole item's copy.
+  // (LDS destinations as integer offsets from the __shared__ objects: no
+  // generic -> LDS pointer conversion per copy)
+  const uint32_t xr_lds = lds_offset(&xr[0][0][0]), ar_lds = lds_offset(&ar[0][0][0]);
+  const uint32_t dr_lds = lds_offset(&dr[0][0][0]);
+  auto issue_copy_part = [&](const Item& r, int b, int m) __attribute__((always_inline)) {
     const int64_t l0 = (int64_t)r.c * kQ;
+    const int hb = 2 * half + b;  // [half][buffer]
     const T* xg = reinterpret_cast<const T*>(p.x) + r.b * p.sxb + l0 * p.sxl + r.h * p.sxh + xcopy;
-#pragma unroll
-    for (int m = 0; m < kXBlocks / kNW; ++m) {
+    {
       const int blk = wave + kNW * m;
-      dma16(xg + (int64_t)(8 * blk) * p.sxl, xr[b] + blk * 512);
+      dma16_at(xg + (int64_t)(8 * blk) * p.sxl, xr_lds + (uint32_t)((hb * kQ * kP + blk * 512) * (int)sizeof(T)));
     }
+    if (m != 0) return;
     if (wave == kNW - 1) {
       const float* ag = p.acs + (((int64_t)r.b * p.nheads + r.h) * p.nchunks + r.c) * kQ;
-      dma16(ag + 4 * lane, ar[b]);
+      dma16_at(ag + 4 * lane, ar_lds + (uint32_t)(hb * kQ * 4));
     }
     if constexpr (HAS_DT) {
       if (wave < kQ / 64) {
         const float* dg = p.dt + r.b * p.sdb + r.h * p.sdh;
-        dma4(dg + (l0 + 64 * wave + lane) * p.sdl, dr[b] + 64 * wave);
+        dma4_at(dg + (l0 + 64 * wave + lane) * p.sdl, dr_lds + (uint32_t)((hb * kQ + 64 * wave) * 4));
       }
     }
   };
 
-  // w[l] = exp(Acs[Q-1] - Acs[l]) dt[l] of the item in buffer b
+  // w[l] = exp(Acs[Q-1] - Acs[l]) dt[l] of the item in this half's buffer b
   auto tabulate = [&](int b) __attribute__((always_inline)) {
-    for (int l = tid; l < kQ; l += kThreads) {
-      float w = __builtin_amdgcn_exp2f((ar[b][kQ - 1] - ar[b][l]) * kLog2e);
-      if constexpr (HAS_DT) w *= dr[b][l];
-      wr[l] = w;
+    for (int l = htid; l < kQ; l += 512) {
+      float w = __builtin_amdgcn_exp2f((ar[half][b][kQ - 1] - ar[half][b][l]) * kLog2e);
+      if constexpr (HAS_DT) w *= dr[half][b][l];
+      wr[half][l] = w;
     }
   };
 
   // ---- per-group registers: B^T fragments of this wave's n tile, one per K step ----
   frag8<T> bt[kKS];
-  auto load_group = [&](int it) __attribute__((always_inline)) {
+  auto load_group = [&](const Item& r) __attribute__((always_inline)) {
     int lane_o = lane;
     asm volatile("" : "+v"(lane_o));  // opaque: per-group address math, not hoisted
     const int go = lane_o >> 4, io = lane_o & 15;
-    const Item r = item_of(p, it);
     if constexpr (PREP) {
       // chunk_prep's fragments: one 16-byte load per K step
       const frag8<T>* bf = reinterpret_cast<const frag8<T>*>(p.btf) +
@@ -156,16 +167,20 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
       for (int j = 0; j < 8; ++j) bt[ks][j] = bg[(int64_t)(32 * ks + slot_token(go, j)) * p.sbl];
   };
 
-  // ---- one item from LDS buffer b into the state registers ----
+  // ---- one item from this half's LDS buffer b into the state registers ----
   f32x4 acc[PTW];
-  auto compute = [&](int b) __attribute__((always_inline)) {
-    const T* xb = xr[b];
+  // step(ks) runs before K step ks.
+  auto compute = [&](int b, auto step) __attribute__((always_inline)) {
+    const T* xb = xr[half][b];
+    const float* wh = wr[half];
 #pragma unroll
     for (int q = 0; q < PTW; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < kKS; ++ks) {
-      const f32x4 w0 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 4 * g);
-      const f32x4 w1 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 16 + 4 * g);
+      set_prio(3 - ks / 2);  // waves behind in the item go first
+      step(ks);
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(wh + 32 * ks + 4 * g);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(wh + 32 * ks + 16 + 4 * g);
       frag8<T> hi, lo;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
@@ -185,35 +200,57 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
   };
 
   f32x4 st_prev[PTW];
-  auto store_states = [&](const Item& r) __attribute__((always_inline)) {
+  auto store_state = [&](const Item& r, int q) __attribute__((always_inline)) {
     S* sg = reinterpret_cast<S*>(p.states) + (((int64_t)r.b * p.nchunks + r.c) * p.nheads + r.h) * (int64_t)(kP * N);
-#pragma unroll
-    for (int q = 0; q < PTW; ++q) StateStore<S>::store(sg + srow + 16 * N * q, st_prev[q]);
+    StateStore<S>::store(sg + srow + 16 * N * q, st_prev[q]);
   };
 
-  Item cur = item_of(p, it0), prev = cur;
-  issue_copy(it0, 0);
-  load_group(it0);
+  // The two halves take alternate items of the range (half h: it0 + h,
+  // it0 + h + 2, ...) and run in lockstep, one barrier pair per step, so
+  // they finish together.  Per step and half: compute the current item while
+  // the next one's copy and the previous one's state stores are issued
+  // between its K steps; then wait for the copy, publish it, tabulate its
+  // weights, and publish those.
+  const int nsteps = (it1 - it0 + 1) / 2;
+  Item cur = item_of(p, it0 + half), prev = cur;
+  const bool any = it0 + half < it1;
+  if (any) {
+#pragma unroll
+    for (int m = 0; m < kXBlocks / kNW; ++m) issue_copy_part(cur, 0, m);
+    load_group(cur);
+  }
   dma_wait();
   __syncthreads();
-  tabulate(0);
+  if (any) tabulate(0);
   __syncthreads();
-  for (int it = it0; it < it1; ++it) {
-    const int bc = (it - it0) & 1, bn = bc ^ 1;
-    const bool has_next = it + 1 < it1;
-    if (has_next) issue_copy(it + 1, bn);
-    if (it > it0) store_states(prev);
-    compute(bc);
+  for (int k = 0; k < nsteps; ++k) {
+    const int it = it0 + half + 2 * k;
+    const int bc = k & 1, bn = bc ^ 1;
+    const bool active = it < it1, has_next = it + 2 < it1;
+    const Item nxt = has_next ? item_of(p, it + 2) : cur;
+    const bool has_prev = k > 0;
+    if (active) {
+      // copy parts in steps 0..3, the previous item's state stores after them
+      compute(bc, [&](int ks) __attribute__((always_inline)) {
+        if (ks < kXBlocks / kNW) {
+          if (has_next) issue_copy_part(nxt, bn, ks);
+        } else if (ks - kXBlocks / kNW < PTW) {
+          if (has_prev) store_state(prev, ks - kXBlocks / kNW);
+        }
+      });
 #pragma unroll
-    for (int q = 0; q < PTW; ++q) st_prev[q] = acc[q];
-    dma_wait();
+      for (int q = 0; q < PTW; ++q) st_prev[q] = acc[q];
+      prev = cur;
+    }
+    // the next item's copy, issued before this step's PTW state stores, must
+    // have landed; the stores may still be in flight
+    if (active && has_prev) vm_wait<PTW>();
+    else dma_wait();
     __syncthreads();
-    prev = cur;
     if (has_next) {
       tabulate(bn);
-      const Item nxt = item_of(p, it + 1);
       if (nxt.b != cur.b || nxt.c != cur.c || nxt.grp != cur.grp) {
-        load_group(it + 1);
+        load_group(nxt);
         // complete before the next item's copies are issued: the compiler's
         // wait before the first use would also count those copies
         dma_wait();
@@ -222,7 +259,10 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
     }
     __syncthreads();
   }
-  store_states(prev);
+  if (any) {
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) store_state(prev, q);
+  }
 }
 
 template <typename T, typename S, int NK>

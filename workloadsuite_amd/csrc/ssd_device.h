@@ -190,6 +190,26 @@ __device__ __forceinline__ void dma4_at(const void* g, uint32_t lds_off) {
 __device__ __forceinline__ void dma4(const void* g, void* lds_base) { dma4_at(g, lds_offset(lds_base)); }
 // s_waitcnt vmcnt(0): every vector memory operation of this wave has completed.
 __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70); }
+// s_waitcnt vmcnt(N): all but this wave's N most recent vector memory
+// operations have completed (the count retires in issue order), e.g. copies
+// issued before N stores, without waiting for the stores.
+template <int N> __device__ __forceinline__ void vm_wait() {
+  static_assert(N >= 0 && N < 16, "vmcnt immediate");
+  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+}
+
+// s_setprio with a value known after unrolling (the builtin takes an
+// immediate).  Kernels whose waves meet at a barrier every item raise the
+// priority of the waves that are behind in the item -- the hardware otherwise
+// favours the oldest waves, and the youngest finish their item alone.
+__device__ __forceinline__ void set_prio(int prio) {
+  switch (prio) {
+    case 3: __builtin_amdgcn_s_setprio(3); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    default: __builtin_amdgcn_s_setprio(0); break;
+  }
+}
 
 // MFMA K slot j of lane group g stands for token 4 g + j (j < 4) or 16 + 4 g + j - 4
 // (j >= 4) of a 32-token step: the rows a pair of transposing reads delivers.
