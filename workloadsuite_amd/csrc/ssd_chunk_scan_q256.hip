@@ -108,15 +108,15 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   static_assert(PPR >= 8 && SCOPIES >= 1 && SCOPIES <= 4, "S_in row shape");
   auto ssw = [](int r) __attribute__((always_inline)) { return PPR >= 16 ? (r & 15) : ((r >> 1) & 7); };
   // Two buffers of each: the current item's and the next item's (in flight).
-  // After an item's compute its x buffer holds that item's y for the stores.
   __shared__ __attribute__((aligned(1024))) T xr[2][kQ * kP];
   __shared__ __attribute__((aligned(1024))) unsigned char sr[2][kP * RB];
   __shared__ __attribute__((aligned(16))) float ar[2][kQ];
-  // G[s] = exp(Acs[r] - Acs[s]), r the last token of s's 32-token block
-  // (written by convert(); the decay of the blocks below the diagonal factors
-  // as exp(Acs[l] - Acs[r]) * G[s]).
-  __shared__ __attribute__((aligned(16))) float gr[2][kQ];
   __shared__ __attribute__((aligned(16))) float dr[HAS_DT ? 2 : 1][HAS_DT ? kQ : 4];
+  // Per-wave tables of the current item (each wave writes and reads only its
+  // own, so they need no barrier): [0] Acs * log2(e); [1] G[s] =
+  // exp(Acs[r] - Acs[s]), r the last token of s's 32-token block (the decay
+  // of the blocks below the diagonal factors as exp(Acs[l] - Acs[r]) * G[s]).
+  __shared__ __attribute__((aligned(16))) float wt[kNW][2][kQ];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   __builtin_assume(wave < kNW);  // lets the tile-range tests below fold
@@ -154,21 +154,17 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   // ---- per-lane parts of the copy and store addresses (fixed for the kernel) ----
   // x copy: lane reads row (lane / 8) of its 8-row block, piece (lane % 8) ^ (lane / 8).
   const int64_t xcopy = (int64_t)(lane >> 3) * p.sxl + 8 * ((lane & 7) ^ (lane >> 3));
-  // y staging in LDS: row l (128 B) keeps the 8 p of piece c at slot
-  // c ^ ((l >> 1) & 7).  A lane writes row 16 t + i, p 16 pt + 4 g .. + 3
-  // (8 bytes); a store copy reads 8 whole rows (1 KB, lane k: row k / 8,
-  // slot k % 8) and writes each row's 128 bytes with 16 bytes per lane.
-  // slot (2 pt + g / 2) ^ ((i >> 1) & 7) = (2 pt) ^ ysw: byte offset of column
-  // tile pt = i 128 + 8 (g & 1) + ((32 pt) ^ (16 ysw))
-  const int ysw = (g >> 1) ^ ((i >> 1) & 7);
-  const int yrow = i * 128 + 8 * (g & 1);
+  // y store: a lane holds p 16 pt + 4 g .. + 3 of row 16 t + i for every
+  // column tile pt; lane rows g, g ^ 1 swap halves of the column-tile pairs
+  // (0, 1) and (2, 3), after which each lane holds 8 consecutive p starting
+  // at 32 pair + ycol of its row (16-byte stores, 64 contiguous bytes per
+  // row and instruction).
+  const int ycol = 8 * (g >> 1) + 16 * (g & 1);
   // S_in copy: lane k fills slot k % PPR of row RPD d + k / PPR, i.e. reads
   // piece (k % PPR) ^ ssw(row); the row's ssw depends on d only through the
   // wave (RPD d = RPD wave mod 16).
   const int scopy = (lane / PPR) * N + ((lane % PPR) ^ ssw(wave * RPD + lane / PPR)) * (16 / (int)sizeof(S));
-  // store copy blk = wave + 8 m: rows 8 blk + lane / 8, and 8 blk is
-  // 8 wave mod 16, so the slot -> piece map depends only on the wave's parity
-  const int64_t ycopy = (int64_t)(lane >> 3) * p.syl + 8 * ((lane & 7) ^ ((4 * (wave & 1) + (lane >> 4)) & 7));
+
 
   // ---- global -> LDS copy of one item's x, S_in, Acs (and dt) into buffer b ----
   // LDS offsets of the buffer arrays (from the __shared__ objects themselves,
@@ -213,19 +209,25 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   static_assert(kXBlocks == 4 * kNW, "four copy parts cover x");
 
 
-  // ---- once the copy of buffer b has landed: Acs *= log2(e); S_in -> MFMA operand type ----
-  // f32 S_in: each 32-byte pair of pieces (8 states) becomes [hi x8 | lo x8] of T in place.
-  // bf16 S_in with f16 inputs: converted to f16 in place.
-  auto convert = [&](int b) __attribute__((always_inline)) {
-    for (int e = tid; e < kQ; e += kThreads) {
-      const float a = ar[b][e] * kLog2e, ar_end = ar[b][e | 31] * kLog2e;
-      gr[b][e] = __builtin_amdgcn_exp2f(ar_end - a);
+  // ---- once the copy of buffer b has landed ----
+  // This wave's tables of the item (no barrier: only this wave reads them).
+  auto tables = [&](int b) __attribute__((always_inline)) {
+#pragma unroll
+    for (int e = lane; e < kQ; e += 64) {
+      const float a = ar[b][e] * kLog2e, a_end = ar[b][e | 31] * kLog2e;
+      wt[wave][0][e] = a;
+      wt[wave][1][e] = __builtin_amdgcn_exp2f(a_end - a);
     }
-    __syncthreads();  // every G read its block's unscaled last Acs
-    for (int e = tid; e < kQ; e += kThreads) ar[b][e] *= kLog2e;
+  };
+  // S_in -> MFMA operand type, by all waves (a barrier publishes it).  f32
+  // S_in: each 32-byte pair of pieces (8 states) becomes [hi x8 | lo x8] of T
+  // in place, unless state_passing already stored it so; bf16 S_in with f16
+  // inputs: converted to f16 in place.
+  constexpr bool kBf16ToF16 = !SPLIT && !std::is_same<S, T>::value;
+  const bool must_convert = SPLIT ? !p.presplit : kBf16ToF16;
+  auto convert = [&](int b) __attribute__((always_inline)) {
     if constexpr (SPLIT) {
-      // (with presplit the copy already holds the pairs)
-      for (int u = p.presplit ? kP * (N / 8) : tid; u < kP * (N / 8); u += kThreads) {
+      for (int u = tid; u < kP * (N / 8); u += kThreads) {
         // pair q = pieces 2q, 2q+1 (8 states) -> hi at piece 2q's slot, lo at 2q+1's
         const int row = u / (N / 8), q = u % (N / 8), sw = ssw(row);
         unsigned char* ph = sr[b] + row * RB + 16 * ((2 * q) ^ sw);
@@ -243,7 +245,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
         *reinterpret_cast<frag8<T>*>(ph) = hi;
         *reinterpret_cast<frag8<T>*>(pl) = lo;
       }
-    } else if constexpr (!std::is_same<S, T>::value) {
+    } else if constexpr (kBf16ToF16) {
       for (int u = tid; u < kP * PPR; u += kThreads) {
         unsigned char* pr = sr[b] + 16 * u;
         const frag8<S> v = *reinterpret_cast<const frag8<S>*>(pr);
@@ -321,8 +323,8 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   auto compute = [&](int b, auto off_step) __attribute__((always_inline)) {
     const T* xb = xr[b];
     const unsigned char* sbuf = sr[b];
-    const float* ab = ar[b];
-    const float* gb = gr[b];
+    const float* ab = wt[wave][0];
+    const float* gb = wt[wave][1];
     const float* db = dr[HAS_DT ? b : 0];
     const int KB = kNPair - KA;
     float al[2];
@@ -433,54 +435,59 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
         for (int jj = 0; jj < 4; ++jj) ypk[s2][pt][jj] = from_f32<T>(acc[s2][pt][jj]);
   };
 
-  // y through LDS: stage_y writes this wave's rows into x buffer b (free once
-  // every wave has computed from it); store_y(r, b, m) reads store copy m
-  // (rows 8 (wave + 8 m) .. + 7) back and writes it to item r's y.
-  auto stage_y = [&](int b) __attribute__((always_inline)) {
-    unsigned char* xb = reinterpret_cast<unsigned char*>(xr[b]);
+  // y of item r from ypk: lane rows g, g ^ 1 swap halves of the column-tile
+  // pairs, then each lane stores 8 consecutive p (16 bytes) of its row.
+  auto store_y = [&](const Item& r) __attribute__((always_inline)) {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    T* yg = reinterpret_cast<T*>(p.y) + (int64_t)r.b * p.syb + ((int64_t)r.c * kQ) * p.syl + (int64_t)r.h * p.syh;
 #pragma unroll
-    for (int pt = 0; pt < 4; ++pt) {
-      const int o = yrow + ((32 * pt) ^ (16 * ysw));
-      *reinterpret_cast<vec4<T>*>(xb + 2048 * ta + o) = ypk[0][pt];
-      *reinterpret_cast<vec4<T>*>(xb + 2048 * tb + o) = ypk[1][pt];
+    for (int s2 = 0; s2 < 2; ++s2) {
+      T* yrow = yg + (int64_t)(16 * (s2 ? tb : ta) + i) * p.syl + ycol;
+#pragma unroll
+      for (int pp = 0; pp < 2; ++pp) {
+        const u32x2 a = __builtin_bit_cast(u32x2, ypk[s2][2 * pp]);
+        const u32x2 c = __builtin_bit_cast(u32x2, ypk[s2][2 * pp + 1]);
+        // row g even keeps tile 2pp and takes the odd row's half of it; row g
+        // odd takes the even row's half of tile 2pp+1 and keeps its own
+        const auto w0 = __builtin_amdgcn_permlane16_swap(a[0], c[0], false, false);
+        const auto w1 = __builtin_amdgcn_permlane16_swap(a[1], c[1], false, false);
+        *reinterpret_cast<u32x4*>(yrow + 32 * pp) = u32x4{w0[0], w1[0], w0[1], w1[1]};
+      }
     }
   };
-  auto store_y = [&](const Item& r, int b, int m) __attribute__((always_inline)) {
-    const unsigned char* xb = reinterpret_cast<const unsigned char*>(xr[b]);
-    const frag8<T> v = *reinterpret_cast<const frag8<T>*>(xb + (wave + kNW * m) * 1024 + 16 * lane);
-    T* yg = reinterpret_cast<T*>(p.y) + (int64_t)r.b * p.syb + ((int64_t)r.c * kQ) * p.syl + (int64_t)r.h * p.syh;
-    *reinterpret_cast<frag8<T>*>(yg + (int64_t)(8 * (wave + kNW * m)) * p.syl + ycopy) = v;
-  };
 
-  // Per item: compute it while the previous item's staged y is stored and
-  // the next item's copy issued (into the same LDS blocks, each read out by
-  // its wave first) between its steps; then wait for the copy, publish it,
-  // stage this item's y, convert the copy, and publish both.
-  Item cur = item_of(p, it0), prev = cur;
+  // Per item: compute it while the next item's copy is issued between its
+  // steps, store its y; then wait for the copy, publish it (the one barrier
+  // per item), and form this wave's tables of the next item.
+  Item cur = item_of(p, it0);
 #pragma unroll
   for (int part = 0; part < 4; ++part) issue_copy_part(cur, 0, part);
   load_group(it0);
   dma_wait();
   __syncthreads();
-  convert(0);
-  __syncthreads();
+  if (must_convert) {
+    convert(0);
+    __syncthreads();
+  }
+  tables(0);
   for (int it = it0; it < it1; ++it) {
     const int bc = (it - it0) & 1, bn = bc ^ 1;
     const bool has_next = it + 1 < it1;
     const Item nxt = has_next ? item_of(p, it + 1) : cur;
-    const bool has_prev = it > it0;
     compute(bc, [&](int pt) __attribute__((always_inline)) {
-      if (has_prev) store_y(prev, bn, pt);
-      // block wave + 8 pt is read out before the copy into it is issued
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       if (has_next) issue_copy_part(nxt, bn, pt);
     });
-    dma_wait();
+    store_y(cur);
+    // the copy has landed; this item's 4 y stores may still be in flight
+    vm_wait<4>();
     __syncthreads();
-    stage_y(bc);
-    prev = cur;
     if (has_next) {
-      convert(bn);
+      if (must_convert) {
+        convert(bn);
+        __syncthreads();
+      }
+      tables(bn);
       if (nxt.b != cur.b || nxt.c != cur.c || nxt.grp != cur.grp) {
         load_group(it + 1);
         // complete before the next item's copies are issued: the compiler's
@@ -489,10 +496,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
       }
       cur = nxt;
     }
-    __syncthreads();
   }
-#pragma unroll
-  for (int m = 0; m < 4; ++m) store_y(prev, (it1 - 1 - it0) & 1, m);
 }
 
 bool fits_i32(int64_t v) { return v >= INT32_MIN && v <= INT32_MAX; }
