@@ -110,12 +110,13 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   // Two buffers of each: the current item's and the next item's (in flight).
   __shared__ __attribute__((aligned(1024))) T xr[2][kQ * kP];
   __shared__ __attribute__((aligned(1024))) unsigned char sr[2][kP * RB];
-  __shared__ __attribute__((aligned(16))) float ar[2][kQ];
   __shared__ __attribute__((aligned(16))) float dr[HAS_DT ? 2 : 1][HAS_DT ? kQ : 4];
-  // Per-wave tables of the current item (each wave writes and reads only its
-  // own, so they need no barrier): [0] Acs * log2(e); [1] G[s] =
+  // Each wave's own copy of the next item's Acs, and its tables of the
+  // current item (a wave writes and reads only its own, so they need no
+  // barrier): [0] Acs * log2(e); [1] G[s] =
   // exp(Acs[r] - Acs[s]), r the last token of s's 32-token block (the decay
   // of the blocks below the diagonal factors as exp(Acs[l] - Acs[r]) * G[s]).
+  __shared__ __attribute__((aligned(16))) float ar[kNW][kQ];
   __shared__ __attribute__((aligned(16))) float wt[kNW][2][kQ];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
@@ -195,9 +196,9 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
       const int d = wave + kNW * part;
       dma16_at(sg + d * RPD * N, sr_lds + (uint32_t)(b * kP * RB + d * 1024));
     }
-    if (part == 0 && wave == kNW - 1) {
+    if (part == 0) {
       const float* ag = p.acs + (((int64_t)r.b * p.nheads + r.h) * p.nchunks + r.c) * kQ;
-      dma16_at(ag + 4 * lane, ar_lds + (uint32_t)(b * kQ * 4));
+      dma16_at(ag + 4 * lane, ar_lds + (uint32_t)(wave * kQ * 4));
     }
     if constexpr (HAS_DT) {
       if (part == 0 && wave < kQ / 64) {
@@ -209,12 +210,12 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   static_assert(kXBlocks == 4 * kNW, "four copy parts cover x");
 
 
-  // ---- once the copy of buffer b has landed ----
-  // This wave's tables of the item (no barrier: only this wave reads them).
-  auto tables = [&](int b) __attribute__((always_inline)) {
+  // ---- once the copy of the next item has landed ----
+  // This wave's tables of the item, from its own copy of Acs (no barrier).
+  auto tables = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int e = lane; e < kQ; e += 64) {
-      const float a = ar[b][e] * kLog2e, a_end = ar[b][e | 31] * kLog2e;
+      const float a = ar[wave][e] * kLog2e, a_end = ar[wave][e | 31] * kLog2e;
       wt[wave][0][e] = a;
       wt[wave][1][e] = __builtin_amdgcn_exp2f(a_end - a);
     }
@@ -458,19 +459,20 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   };
 
   // Per item: compute it while the next item's copy is issued between its
-  // steps, store its y; then wait for the copy, publish it (the one barrier
-  // per item), and form this wave's tables of the next item.
+  // steps, store its y; then wait for the copy, form this wave's tables of
+  // the next item (from its own copy of Acs) and publish the copy (the one
+  // barrier per item).
   Item cur = item_of(p, it0);
 #pragma unroll
   for (int part = 0; part < 4; ++part) issue_copy_part(cur, 0, part);
   load_group(it0);
   dma_wait();
+  tables();
   __syncthreads();
   if (must_convert) {
     convert(0);
     __syncthreads();
   }
-  tables(0);
   for (int it = it0; it < it1; ++it) {
     const int bc = (it - it0) & 1, bn = bc ^ 1;
     const bool has_next = it + 1 < it1;
@@ -481,13 +483,13 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     store_y(cur);
     // the copy has landed; this item's 4 y stores may still be in flight
     vm_wait<4>();
+    if (has_next) tables();
     __syncthreads();
     if (has_next) {
       if (must_convert) {
         convert(bn);
         __syncthreads();
       }
-      tables(bn);
       if (nxt.b != cur.b || nxt.c != cur.c || nxt.grp != cur.grp) {
         load_group(it + 1);
         // complete before the next item's copies are issued: the compiler's
