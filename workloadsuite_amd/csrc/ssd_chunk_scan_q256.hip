@@ -374,9 +374,19 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
         int lane_o = lane;
         asm volatile("" : "+v"(lane_o));
         const int go = lane_o >> 4, l = 16 * (s2 ? tb : ta) + (lane_o & 15);
-        // exact decay, masked before it can overflow above the diagonal
+        // Exact decay, masked before it can overflow above the diagonal.  The
+        // sub-tile of rows 16 t .. 16 t + 15 crosses the diagonal; for even t
+        // the other one lies wholly above it (zero), for odd t wholly below
+        // it (no mask needed).
+        const bool odd = ((s2 ? tb : ta) & 1) != 0;  // wave-uniform
+        f32x8 wv;
 #pragma unroll
         for (int st = 0; st < 2; ++st) {
+          if (!odd && st == 1) {
+#pragma unroll
+            for (int jj = 0; jj < 4; ++jj) wv[4 + jj] = 0.f;
+            continue;
+          }
           const f32x4 as = *reinterpret_cast<const f32x4*>(ab + 32 * sb + 16 * st + 4 * g);
           f32x4 ds = f32x4{1.f, 1.f, 1.f, 1.f};
           if constexpr (HAS_DT) ds = *reinterpret_cast<const f32x4*>(db + 32 * sb + 16 * st + 4 * g);
@@ -384,9 +394,11 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
           for (int jj = 0; jj < 4; ++jj) {
             float w = __builtin_amdgcn_exp2f(al[s2] - as[jj]) * cb[st][jj];
             if constexpr (HAS_DT) w *= ds[jj];
-            af[4 * st + jj] = from_f32<T>((32 * sb + 16 * st + 4 * go + jj <= l) ? w : 0.f);
+            const bool below = odd && st == 0;
+            wv[4 * st + jj] = (below || 32 * sb + 16 * st + 4 * go + jj <= l) ? w : 0.f;
           }
         }
+        af = __builtin_convertvector(wv, frag8<T>);
       } else {
         // below the diagonal: exp(Acs[l] - Acs[s]) = exp(Acs[l] - Acs[r]) G[s]
         const float fl = __builtin_amdgcn_exp2f(al[s2] - ab[32 * sb + 31]);

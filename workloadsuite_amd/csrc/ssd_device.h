@@ -194,8 +194,9 @@ __device__ __forceinline__ void dma_wait() { __builtin_amdgcn_s_waitcnt(0x0F70);
 // operations have completed (the count retires in issue order), e.g. copies
 // issued before N stores, without waiting for the stores.
 template <int N> __device__ __forceinline__ void vm_wait() {
-  static_assert(N >= 0 && N < 16, "vmcnt immediate");
-  __builtin_amdgcn_s_waitcnt(0x0F70 | N);
+  static_assert(N >= 0 && N < 64, "vmcnt immediate");
+  // vmcnt is split over bits [3:0] and [15:14]
+  __builtin_amdgcn_s_waitcnt(0x0F70 | (N & 15) | ((N >> 4) << 14));
 }
 
 // s_setprio with a value known after unrolling (the builtin takes an
