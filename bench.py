@@ -3,6 +3,7 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3]
                     [--state-dtype f32|bf16] [--no-cpu-baseline]
+    python bench.py --layer [--steps K] [--warmup W]
 
 A step is one SSD forward (K1 cumsum -> K0 chunk_prep -> K2 chunk_state ->
 K3 state_passing -> K4 chunk_scan) over one batch of synthetic inputs already resident in HBM, at
@@ -18,6 +19,14 @@ algorithmic bytes (or flops) per launch over that duration give
 ``roofline.achieved``.  ``cpu_baseline`` times the CPU oracle's float32
 restatement of the reference einsum path on a bounded sample (one batch
 element of the same config) on this host's cores.
+
+``--layer`` instead times one full Mamba-2 layer at the reference module's
+production shape (workloads/mamba/model_ref.py:209-221: batch 8, seqlen 2048,
+d_model 2048, 128 heads, d_state 128, 8 groups, block_len 64, fp16, random
+weights): the whole ``SSDLayer.forward``, and separately the span between
+its two projections, once as libssd's single ``ssd_layer`` call and once as
+PyTorch glue (conv1d, SiLU, softplus, skip, gate) around ``ssd_forward``.
+It prints one JSON line of its own; the headline line above is unaffected.
 """
 
 from __future__ import annotations
@@ -154,6 +163,66 @@ def cpu_baseline(cfg, budget_s=12.0, max_runs=30):
     }
 
 
+def layer_bench(args):
+    import torch.nn.functional as F
+
+    from workloadsuite_amd import mamba_layer as ML
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    torch.manual_seed(0)
+    d_model, _, h, N, P, g, Q, k = ML.get_init_inputs()
+    b, L = ML.batch_size, ML.seq_length
+    layer = ML.SSDLayer(d_model, h, N, P, g, block_len=Q, conv_kernel=k).to(dev).eval()
+    u = torch.randn(b, L, d_model, dtype=torch.float16, device=dev)
+    d_inner = h * P
+    with torch.inference_mode():
+        zxbcdt = layer.in_proj(layer.norm(u))
+        x, z, B, C, dt = torch.split(zxbcdt, [d_inner, d_inner, g * N, g * N, h], dim=-1)
+        Bv, Cv = B.view(b, L, g, N), C.view(b, L, g, N)
+
+        def fused():
+            return S.ssd_layer(x, z, Bv, Cv, dt, layer.conv1d.weight, layer.conv1d.bias, layer.dt_bias,
+                               layer.A_log, layer.D, Q, h)
+
+        def glue():
+            xx = F.silu(layer.conv1d(x.transpose(1, 2))[..., :L]).transpose(1, 2).contiguous()
+            X = xx.view(b, L, h, P)
+            dtt = F.softplus(dt + layer.dt_bias)
+            Y = S.ssd_forward(X, -torch.exp(layer.A_log) * dtt.float(), Bv, Cv, Q, dt=dtt.float())
+            Y = Y + X * layer.D.view(1, 1, -1, 1)
+            return Y.reshape(b, L, d_inner) * F.silu(z)
+
+        def whole():
+            return layer(u)
+
+        diff = (fused().float() - glue().float()).abs().max().item()
+        res = {}
+        for name, fn in (("layer", whole), ("span_fused", fused), ("span_torch_glue", glue)):
+            for _ in range(args.warmup):
+                fn()
+            res[name] = time_launches(fn, args.steps)
+    tokens = b * L
+    out = {
+        "metric": "Mamba-2 SSD layer forward tokens/s (one layer, model_ref.py production shape), 1 MI355X",
+        "value": round(tokens / (res["layer"] * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(res["layer"], 5),
+        "higher_is_better": True,
+        "dtype": "f16",
+        "data": "synthetic (u ~ N(0,1); module's default init)",
+        "config": {"workload": "mamba2-layer R0", "batch": b, "seqlen": L, "d_model": d_model, "nheads": h,
+                   "headdim": P, "dstate": N, "ngroups": g, "chunk": Q, "conv_kernel": k},
+        "span_ms": {"ssd_layer (fused)": round(res["span_fused"], 5),
+                    "torch glue + ssd_forward": round(res["span_torch_glue"], 5)},
+        "span_max_abs_diff": diff,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -163,6 +232,8 @@ def main():
     ap.add_argument("--state-dtype", default="f32", choices=["f32", "bf16"])
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=30)
+    ap.add_argument("--layer", action="store_true",
+                    help="time one full layer at the reference module's production shape instead")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="only run a plain device-to-device copy of MB MiB (5 times) and exit: the "
                          "reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -173,6 +244,10 @@ def main():
               "shards over batch x heads with no communication, so N GPUs would each run this "
               "single-GPU workload on 1/N of the heads.", file=sys.stderr)
         sys.exit(2)
+
+    if args.layer:
+        layer_bench(args)
+        return
 
     if args.copy_probe:
         n = args.copy_probe << 20

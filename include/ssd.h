@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SSD_ABI_VERSION 2
+#define SSD_ABI_VERSION 3
 
 /* Element types.  The two SPLIT values are a storage format of the per-chunk
  * states only: each f32 state as the 16-bit pair hi = round(v),
@@ -73,6 +73,7 @@ enum {
   SSD_ERR_MISALIGNED = -10,          /* vector-loaded rows not 16-byte aligned */
   SSD_ERR_WORKSPACE_TOO_SMALL = -11,
   SSD_ERR_TOO_LARGE = -12,           /* a grid dimension would overflow        */
+  SSD_ERR_UNSUPPORTED_CONV = -13,    /* conv kernel width not in 1..4          */
 };
 
 /* Problem dimensions. */
@@ -145,12 +146,25 @@ int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype,
                       const float* chunk_decay, const float* initial_states,
                       float* final_states, void* stream);
 
+/* Skip and gate of SSDLayer.forward (MR:116-118), applied by ssd_chunk_scan
+ * to y in float32 before its single rounding to the output dtype:
+ *   y[l,p] = (y_ssd[l,p] + D[h] x[l,p]) * silu(z[l,p]),  silu(v) = v / (1 + e^-v)
+ * D: [h] f32, or NULL (no skip term).  z: [b, L, h, P] of the input dtype
+ * with element strides z_strides (unit stride over P), or NULL (no gate). */
+typedef struct ssd_epilogue {
+  const float* D;
+  const void* z;
+  int64_t z_strides[4];
+} ssd_epilogue;
+
 /* K4 -- fused chunk scan: writes y once,
  *   y[l,p] = sum_{s<=l} exp(Acs[l]-Acs[s]) (C_l.B_s) dt[s] x[s,p]
  *            + exp(Acs[l]) sum_n C[l,n] states[c][p,n].
  * Replaces MR:139-145 (segsum, mask, C.B^T, Y_diag), MR:160-161 (Y_off) and
  * MR:162 (the sum).
- * prep: NULL, or ssd_chunk_prep's output for the same d, dtype, bmat, cmat. */
+ * prep: NULL, or ssd_chunk_prep's output for the same d, dtype, bmat, cmat.
+ * epilogue: NULL (y as above, MR's _ssd_core), or the layer's skip and gate
+ * (MR:116-118) fused into the same write of y. */
 int ssd_chunk_scan(const ssd_dims* d, int dtype,
                    const void* x, const int64_t x_strides[4],
                    const void* bmat, const int64_t b_strides[4],
@@ -158,7 +172,7 @@ int ssd_chunk_scan(const ssd_dims* d, int dtype,
                    const float* dt, const int64_t dt_strides[3],
                    const float* a_cumsum, const void* states, int state_dtype,
                    void* y, const int64_t y_strides[4],
-                   const void* prep, void* stream);
+                   const void* prep, const ssd_epilogue* epilogue, void* stream);
 
 /* Whole SSD forward (K1, K0, K2, K3, K4 on one stream): the replacement for
  * SSDLayer._ssd_core (MR:123-162).  workspace must hold
@@ -174,6 +188,55 @@ int ssd_forward(const ssd_dims* d, int dtype,
                 float* final_states,
                 void* workspace, size_t workspace_bytes, int state_dtype,
                 void* stream);
+
+/* ---- the layer around the SSD core (SSDLayer.forward, MR:68-121) ---- */
+
+/* Parameters of one layer, as MR's module holds them (MR:41-66).  Device
+ * pointers; conv_w, conv_b and dt_bias are of the layer's dtype (MR: f16). */
+typedef struct ssd_layer_params {
+  int64_t conv_kernel;  /* k, 1..4 (MR default 4) */
+  const void* conv_w;   /* conv1d.weight [h*P, 1, k], contiguous */
+  const void* conv_b;   /* conv1d.bias [h*P], or NULL */
+  const void* dt_bias;  /* [h] */
+  const float* A_log;   /* [h] f32; A = -exp(A_log) (MR:102) */
+  const float* D;       /* [h] f32 skip weight, or NULL (no skip term) */
+} ssd_layer_params;
+
+/* Pre-SSD prep (MR:83-103) in two launches:
+ *   x_out[b,l,h,p] = silu(conv_b[d] + sum_j conv_w[d,j] x_in[b, l-(k-1)+j, d]),
+ *                    d = h P + p, x_in = 0 before l = 0 (causal conv1d, MR:83-86)
+ *   dt_out[b,l,h]  = softplus(dt_in[b,l,h] + dt_bias[h])          (MR:94)
+ *   a_cumsum, chunk_decay as ssd_chunk_cumsum of A_dt = -exp(A_log[h]) dt  (MR:102-103)
+ * x_in [b, L, h*P] and dt_in [b, L, h] are of dtype (MR: strided slices of
+ * in_proj's output) with element strides x_strides / dt_strides (unit stride
+ * over the last dim); x_out [b, L, h, P] dtype and dt_out [b, L, h] f32 are
+ * contiguous.  softplus is log(1 + e^v), and v itself above 20 (torch's
+ * threshold).  Accumulates and activates in float32, rounds x once. */
+int ssd_layer_prep(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
+                   const void* x_in, const int64_t x_strides[3],
+                   const void* dt_in, const int64_t dt_strides[3],
+                   void* x_out, float* dt_out, float* a_cumsum, float* chunk_decay,
+                   void* stream);
+
+/* Workspace of ssd_layer_forward: x_out, dt_out, then ssd_workspace_bytes
+ * (f32 states), each 256-byte aligned; 0 when dims are invalid. */
+size_t ssd_layer_workspace_bytes(const ssd_dims* d, int dtype);
+
+/* SSDLayer.forward between its two projections (MR:76-118): from in_proj's
+ * output slices x_in [b, L, h*P], z [b, L, h*P], bmat/cmat [b, L, g, N] and
+ * dt_in [b, L, h] (all of dtype, any strides with unit innermost stride) to
+ * out_proj's input y [b, L, h*P]:
+ *   ssd_layer_prep, then the SSD core (K0, K2, K3, K4 of ssd_forward), with
+ *   the skip D x and the gate silu(z) fused into K4's write of y.
+ * z_strides / y_strides are over [b, L, h*P]. */
+int ssd_layer_forward(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
+                      const void* x_in, const int64_t x_strides[3],
+                      const void* z, const int64_t z_strides[3],
+                      const void* bmat, const int64_t b_strides[4],
+                      const void* cmat, const int64_t c_strides[4],
+                      const void* dt_in, const int64_t dt_strides[3],
+                      void* y, const int64_t y_strides[3],
+                      void* workspace, size_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

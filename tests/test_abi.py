@@ -151,3 +151,40 @@ def test_python_op_shape_errors_mirror_reference(kw, msg):
 def test_unsupported_dstate_raises_library_error():
     with pytest.raises(S.SSDError, match="d_state"):
         S.workspace_bytes(1, 64, 2, 64, 48, 1, 64)
+
+
+def test_layer_entry_points_validate_on_the_host():
+    lib = _lib.load()
+    dims = d()
+    fake = ctypes.c_void_p(0x100000)
+    s3 = (ctypes.c_int64 * 3)(256 * 1000, 1000, 1)
+    bs4 = (ctypes.c_int64 * 4)(256 * 1000, 1000, 64, 1)
+    prm = _lib.SSDLayerParams(5, 0x100000, 0, 0x100000, 0x100000, 0)
+    args = (fake, s3, fake, s3, fake, fake, fake, fake, None)
+    assert lib.ssd_layer_prep(ctypes.byref(dims), 2, ctypes.byref(prm), *args) == -13
+    prm.conv_kernel = 0
+    assert lib.ssd_layer_prep(ctypes.byref(dims), 2, ctypes.byref(prm), *args) == -13
+    prm.conv_kernel = 4
+    prm.conv_w = None
+    assert lib.ssd_layer_prep(ctypes.byref(dims), 2, ctypes.byref(prm), *args) == -1
+    prm.conv_w = 0x100000
+    assert lib.ssd_layer_prep(ctypes.byref(dims), 2, None, *args) == -1
+    # x_out must be 16-byte aligned for the kernels that read it
+    assert lib.ssd_layer_prep(ctypes.byref(dims), 2, ctypes.byref(prm), fake, s3, fake, s3,
+                              ctypes.c_void_p(0x100008), fake, fake, fake, None) == -10
+    # bad x stride
+    bad = (ctypes.c_int64 * 3)(256 * 1000, 1000, 2)
+    assert lib.ssd_layer_prep(ctypes.byref(dims), 2, ctypes.byref(prm), fake, bad, fake, s3,
+                              fake, fake, fake, fake, None) == -9
+    # workspace: x (f16) and dt (f32) ahead of the core's f32-state workspace
+    n = lib.ssd_layer_workspace_bytes(ctypes.byref(dims), 2)
+    tokens = 2 * 256
+    assert n == tokens * 8 * 64 * 2 + tokens * 8 * 4 + lib.ssd_workspace_bytes(ctypes.byref(dims), 0)
+    ys = (ctypes.c_int64 * 3)(256 * 512, 512, 1)
+    fwd = lambda ws, nb: lib.ssd_layer_forward(ctypes.byref(dims), 2, ctypes.byref(prm), fake, s3, fake, s3,  # noqa: E731
+                                               fake, bs4, fake, bs4, fake, s3, fake, ys, ws, nb, None)
+    assert fwd(fake, n - 1) == -11
+    assert fwd(ctypes.c_void_p(0x100010), n) == -10
+    assert fwd(None, n) == -1
+    prm.conv_kernel = 7
+    assert fwd(fake, n) == -13

@@ -15,7 +15,7 @@ import torch  # noqa: F401  -- must precede the CDLL, see module docstring
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssd.so")
 
-SSD_ABI_VERSION = 2
+SSD_ABI_VERSION = 3
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 STATE_SPLIT_BF16, STATE_SPLIT_F16 = 3, 4  # f32 states as 16-bit (hi, lo) pairs
 
@@ -32,6 +32,9 @@ EXPORTS = (
     "ssd_state_passing",
     "ssd_chunk_scan",
     "ssd_forward",
+    "ssd_layer_prep",
+    "ssd_layer_workspace_bytes",
+    "ssd_layer_forward",
 )
 
 
@@ -40,9 +43,20 @@ class SSDDims(ctypes.Structure):
                 ("batch", "seqlen", "nheads", "headdim", "dstate", "ngroups", "chunk")]
 
 
+class SSDEpilogue(ctypes.Structure):
+    _fields_ = [("D", ctypes.c_void_p), ("z", ctypes.c_void_p), ("z_strides", ctypes.c_int64 * 4)]
+
+
+class SSDLayerParams(ctypes.Structure):
+    _fields_ = [("conv_kernel", ctypes.c_int64), ("conv_w", ctypes.c_void_p), ("conv_b", ctypes.c_void_p),
+                ("dt_bias", ctypes.c_void_p), ("A_log", ctypes.c_void_p), ("D", ctypes.c_void_p)]
+
+
 _i64p = ctypes.POINTER(ctypes.c_int64)
 _vp = ctypes.c_void_p
 _dims_p = ctypes.POINTER(SSDDims)
+_epi_p = ctypes.POINTER(SSDEpilogue)
+_prm_p = ctypes.POINTER(SSDLayerParams)
 _int = ctypes.c_int
 
 _SIGNATURES = {
@@ -56,9 +70,13 @@ _SIGNATURES = {
     "ssd_chunk_state": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _int, _vp, _vp]),
     "ssd_state_passing": (_int, [_dims_p, _vp, _int, _vp, _vp, _vp, _vp]),
     "ssd_chunk_scan": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
-                              _vp, _vp, _int, _vp, _i64p, _vp, _vp]),
+                              _vp, _vp, _int, _vp, _i64p, _vp, _epi_p, _vp]),
     "ssd_forward": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                            _vp, _vp, _i64p, _vp, _vp, ctypes.c_size_t, _int, _vp]),
+    "ssd_layer_prep": (_int, [_dims_p, _int, _prm_p, _vp, _i64p, _vp, _i64p, _vp, _vp, _vp, _vp, _vp]),
+    "ssd_layer_workspace_bytes": (ctypes.c_size_t, [_dims_p, _int]),
+    "ssd_layer_forward": (_int, [_dims_p, _int, _prm_p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                                 _vp, _i64p, _vp, _i64p, _vp, ctypes.c_size_t, _vp]),
 }
 
 _LIB = None

@@ -15,6 +15,7 @@ namespace {
 using ssd::ChunkPrepArgs;
 using ssd::ChunkScanArgs;
 using ssd::ChunkStateArgs;
+using ssd::ConvArgs;
 using ssd::CumsumArgs;
 using ssd::StatePassingArgs;
 
@@ -239,6 +240,146 @@ ChunkScanArgs make_scan_args(const ssd_dims* d, const void* x, const int64_t x_s
   return p;
 }
 
+// The epilogue's operands: D any f32 array, z a [b, L, h, P] operand of the
+// input dtype with unit inner stride (read per element, or 16 bytes at a
+// time where aligned).
+int check_epilogue(const ssd_epilogue* e, int dtype) {
+  if (!e) return SSD_OK;
+  if (e->D && (reinterpret_cast<uintptr_t>(e->D) & 3u) != 0) return SSD_ERR_MISALIGNED;
+  if (e->z) {
+    if (e->z_strides[3] != 1) return SSD_ERR_BAD_STRIDE;
+    for (int k = 0; k < 3; ++k)
+      if (e->z_strides[k] < 0) return SSD_ERR_BAD_STRIDE;
+    if ((reinterpret_cast<uintptr_t>(e->z) % elem_size(dtype)) != 0) return SSD_ERR_MISALIGNED;
+  }
+  return SSD_OK;
+}
+
+void set_epilogue(ChunkScanArgs& p, const ssd_epilogue* e) {
+  if (!e) return;
+  p.dskip = e->D;
+  p.z = e->z;
+  if (e->z) {
+    p.szb = e->z_strides[0];
+    p.szl = e->z_strides[1];
+    p.szh = e->z_strides[2];
+  }
+}
+
+// K0 (when it applies), K2, K3, K4 of one forward, after K1 has written acs
+// and decay.  Operands are validated by the caller.
+int run_core(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4], const void* bmat,
+             const int64_t b_strides[4], const void* cmat, const int64_t c_strides[4], const float* dt,
+             const int64_t dt_strides[3], const float* initial_states, void* y, const int64_t y_strides[4],
+             float* final_states, char* ws, const WsLayout& w, int state_dtype, const ssd_epilogue* epi,
+             hipStream_t s) {
+  int rc;
+  float* acs = reinterpret_cast<float*>(ws + w.acs);
+  float* decay = reinterpret_cast<float*>(ws + w.decay);
+  void* states = ws + w.states;
+  ChunkStateArgs sa = make_state_args(d, x, x_strides, bmat, b_strides, dt, dt_strides, acs, states);
+  ChunkScanArgs ca = make_scan_args(d, x, x_strides, bmat, b_strides, cmat, c_strides, dt, dt_strides, acs, states,
+                                    y, y_strides);
+  set_epilogue(ca, epi);
+  // K0: the persistent kernels' per-group operands, once per (b, c, group)
+  if (prep_applies(d, dtype)) {
+    void* prep = ws + w.prep;
+    if ((rc = hip_status(ssd::launch_chunk_prep(make_prep_args(d, bmat, b_strides, cmat, c_strides, prep), dtype, s))))
+      return rc;
+    sa.btf = prep_btf(d, prep);
+    ca.cbf = prep_cbf(prep);
+  }
+  if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, state_dtype, s)))) return rc;
+  // f32 states for the chunk-256 chunk_scan: K3 writes them as its hi/lo operand pairs
+  StatePassingArgs pa = make_sp_args(d, states, decay, initial_states, final_states);
+  if (state_dtype == SSD_DTYPE_F32 && prep_applies(d, dtype) && ssd::chunk_scan_persistent_supported(ca, dtype)) {
+    pa.split_dtype = dtype;
+    ca.presplit = true;
+  }
+  if ((rc = hip_status(ssd::launch_state_passing(pa, state_dtype, s)))) return rc;
+  return hip_status(ssd::launch_chunk_scan(ca, dtype, state_dtype, s));
+}
+
+// ---- the layer around the core ----
+
+struct LayerWs {
+  size_t xo, dto, core, total;
+  WsLayout cw;
+};
+
+LayerWs layer_ws(const ssd_dims* d, int dtype) {
+  LayerWs w;
+  const size_t tokens = (size_t)d->batch * d->seqlen;
+  w.xo = 0;
+  w.dto = round_up(tokens * d->nheads * d->headdim * elem_size(dtype));
+  w.core = w.dto + round_up(tokens * d->nheads * sizeof(float));
+  w.cw = ws_layout(d, SSD_DTYPE_F32);
+  w.total = w.core + w.cw.total;
+  return w;
+}
+
+int check_layer_params(const ssd_layer_params* prm) {
+  if (!prm) return SSD_ERR_NULL_POINTER;
+  if (prm->conv_kernel < 1 || prm->conv_kernel > 4) return SSD_ERR_UNSUPPORTED_CONV;
+  if (!prm->conv_w || !prm->dt_bias || !prm->A_log) return SSD_ERR_NULL_POINTER;
+  if ((reinterpret_cast<uintptr_t>(prm->A_log) & 3u) != 0 ||
+      (prm->D && (reinterpret_cast<uintptr_t>(prm->D) & 3u) != 0))
+    return SSD_ERR_MISALIGNED;
+  return SSD_OK;
+}
+
+// A [b, L, inner] operand read per element (or per vector where aligned).
+int check_rows3(const void* p, const int64_t* strides, int dtype) {
+  if (!p || !strides) return SSD_ERR_NULL_POINTER;
+  if (strides[2] != 1) return SSD_ERR_BAD_STRIDE;
+  if (strides[0] < 0 || strides[1] < 0) return SSD_ERR_BAD_STRIDE;
+  if ((reinterpret_cast<uintptr_t>(p) % elem_size(dtype)) != 0) return SSD_ERR_MISALIGNED;
+  return SSD_OK;
+}
+
+// Grid limits of the conv and cumsum launches.
+int check_layer_grid(const ssd_dims* d) {
+  const int64_t runs = (d->seqlen + 31) / 32;
+  if (d->batch > 65535 || (runs + 3) / 4 > 65535) return SSD_ERR_TOO_LARGE;
+  return SSD_OK;
+}
+
+int launch_layer_prep(const ssd_dims* d, int dtype, const ssd_layer_params* prm, const void* x_in,
+                      const int64_t x_strides[3], const void* dt_in, const int64_t dt_strides[3], void* x_out,
+                      float* dt_out, float* acs, float* decay, hipStream_t s) {
+  ConvArgs cv;
+  cv.x = x_in;
+  cv.sxb = x_strides[0];
+  cv.sxl = x_strides[1];
+  cv.w = prm->conv_w;
+  cv.bias = prm->conv_b;
+  cv.y = x_out;
+  cv.batch = (int)d->batch;
+  cv.seqlen = (int)d->seqlen;
+  cv.channels = (int)(d->nheads * d->headdim);
+  cv.kwidth = (int)prm->conv_kernel;
+  int rc;
+  if ((rc = hip_status(ssd::launch_conv_silu(cv, dtype, s)))) return rc;
+  CumsumArgs ca;
+  ca.a = nullptr;
+  ca.sab = ca.sal = ca.sah = 0;
+  ca.acs = acs;
+  ca.decay = decay;
+  ca.batch = (int)d->batch;
+  ca.nchunks = (int)(d->seqlen / d->chunk);
+  ca.nheads = (int)d->nheads;
+  ca.chunk = (int)d->chunk;
+  ca.dt_raw = dt_in;
+  ca.srb = dt_strides[0];
+  ca.srl = dt_strides[1];
+  ca.srh = dt_strides[2];
+  ca.dt_bias = prm->dt_bias;
+  ca.a_log = prm->A_log;
+  ca.dt_out = dt_out;
+  ca.raw_dtype = dtype;
+  return hip_status(ssd::launch_chunk_cumsum(ca, s));
+}
+
 }  // namespace
 
 namespace ssd {
@@ -279,6 +420,7 @@ const char* ssd_strerror(int status) {
     case SSD_ERR_MISALIGNED: return "vector-loaded operands need 16-byte aligned rows and buffers";
     case SSD_ERR_WORKSPACE_TOO_SMALL: return "workspace too small (see ssd_workspace_bytes)";
     case SSD_ERR_TOO_LARGE: return "problem too large for 32-bit workgroup indexing";
+    case SSD_ERR_UNSUPPORTED_CONV: return "unsupported conv kernel width (1 to 4)";
     default: break;
   }
   if (status > 0) return hipGetErrorString((hipError_t)status);
@@ -369,7 +511,8 @@ int ssd_chunk_scan(const ssd_dims* d, int dtype, const void* x, const int64_t x_
                    const void* bmat, const int64_t b_strides[4], const void* cmat,
                    const int64_t c_strides[4], const float* dt, const int64_t dt_strides[3],
                    const float* a_cumsum, const void* states, int state_dtype, void* y,
-                   const int64_t y_strides[4], const void* prep, void* stream) {
+                   const int64_t y_strides[4], const void* prep, const ssd_epilogue* epilogue,
+                   void* stream) {
   int rc = check_dims_impl(d, dtype);
   if (rc) return rc;
   const int split = split_of(state_dtype);
@@ -380,9 +523,11 @@ int ssd_chunk_scan(const ssd_dims* d, int dtype, const void* x, const int64_t x_
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
   if (!a_cumsum || !states) return SSD_ERR_NULL_POINTER;
   if ((rc = check_output(y, y_strides, dtype))) return rc;
+  if ((rc = check_epilogue(epilogue, dtype))) return rc;
   if (prep && (reinterpret_cast<uintptr_t>(prep) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
   ChunkScanArgs p = make_scan_args(d, x, x_strides, bmat, b_strides, cmat, c_strides, dt, dt_strides, a_cumsum,
                                    states, y, y_strides);
+  set_epilogue(p, epilogue);
   if (prep_applies(d, dtype)) p.cbf = prep_cbf(prep);
   if (split) {
     // only the chunk-256 kernel reads split states
@@ -419,29 +564,82 @@ int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_str
   char* ws = static_cast<char*>(workspace);
   float* acs = reinterpret_cast<float*>(ws + w.acs);
   float* decay = reinterpret_cast<float*>(ws + w.decay);
-  void* states = ws + w.states;
-  ChunkStateArgs sa = make_state_args(d, x, x_strides, bmat, b_strides, dt, dt_strides, acs, states);
-  ChunkScanArgs ca = make_scan_args(d, x, x_strides, bmat, b_strides, cmat, c_strides, dt, dt_strides, acs, states,
-                                    y, y_strides);
-  const hipStream_t s = (hipStream_t)stream;
   if ((rc = ssd_chunk_cumsum(d, a, a_strides, acs, decay, stream))) return rc;
-  // K0: the persistent kernels' per-group operands, once per (b, c, group)
-  if (prep_applies(d, dtype)) {
-    void* prep = ws + w.prep;
-    if ((rc = hip_status(ssd::launch_chunk_prep(make_prep_args(d, bmat, b_strides, cmat, c_strides, prep), dtype, s))))
-      return rc;
-    sa.btf = prep_btf(d, prep);
-    ca.cbf = prep_cbf(prep);
-  }
-  if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, state_dtype, s)))) return rc;
-  // f32 states for the chunk-256 chunk_scan: K3 writes them as its hi/lo operand pairs
-  StatePassingArgs pa = make_sp_args(d, states, decay, initial_states, final_states);
-  if (state_dtype == SSD_DTYPE_F32 && prep_applies(d, dtype) && ssd::chunk_scan_persistent_supported(ca, dtype)) {
-    pa.split_dtype = dtype;
-    ca.presplit = true;
-  }
-  if ((rc = hip_status(ssd::launch_state_passing(pa, state_dtype, s)))) return rc;
-  return hip_status(ssd::launch_chunk_scan(ca, dtype, state_dtype, s));
+  return run_core(d, dtype, x, x_strides, bmat, b_strides, cmat, c_strides, dt, dt_strides, initial_states, y,
+                  y_strides, final_states, ws, w, state_dtype, nullptr, (hipStream_t)stream);
+}
+
+int ssd_layer_prep(const ssd_dims* d, int dtype, const ssd_layer_params* prm, const void* x_in,
+                   const int64_t x_strides[3], const void* dt_in, const int64_t dt_strides[3], void* x_out,
+                   float* dt_out, float* a_cumsum, float* chunk_decay, void* stream) {
+  int rc = check_dims_impl(d, dtype);
+  if (rc) return rc;
+  if ((rc = check_layer_params(prm))) return rc;
+  if ((rc = check_layer_grid(d))) return rc;
+  if ((rc = check_rows3(x_in, x_strides, dtype))) return rc;
+  if (!dt_in || !dt_strides) return SSD_ERR_NULL_POINTER;
+  for (int k = 0; k < 3; ++k)
+    if (dt_strides[k] < 0) return SSD_ERR_BAD_STRIDE;
+  if ((reinterpret_cast<uintptr_t>(dt_in) % elem_size(dtype)) != 0) return SSD_ERR_MISALIGNED;
+  if (!x_out || !dt_out || !a_cumsum || !chunk_decay) return SSD_ERR_NULL_POINTER;
+  if (!aligned16(x_out) || (reinterpret_cast<uintptr_t>(dt_out) & 3u) != 0) return SSD_ERR_MISALIGNED;
+  return launch_layer_prep(d, dtype, prm, x_in, x_strides, dt_in, dt_strides, x_out, dt_out, a_cumsum,
+                           chunk_decay, (hipStream_t)stream);
+}
+
+size_t ssd_layer_workspace_bytes(const ssd_dims* d, int dtype) {
+  if (check_dims_impl(d, dtype) != SSD_OK) return 0;
+  return layer_ws(d, dtype).total;
+}
+
+int ssd_layer_forward(const ssd_dims* d, int dtype, const ssd_layer_params* prm, const void* x_in,
+                      const int64_t x_strides[3], const void* z, const int64_t z_strides[3], const void* bmat,
+                      const int64_t b_strides[4], const void* cmat, const int64_t c_strides[4], const void* dt_in,
+                      const int64_t dt_strides[3], void* y, const int64_t y_strides[3], void* workspace,
+                      size_t workspace_bytes, void* stream) {
+  int rc = check_dims_impl(d, dtype);
+  if (rc) return rc;
+  if ((rc = check_layer_params(prm))) return rc;
+  if ((rc = check_layer_grid(d))) return rc;
+  if (!workspace) return SSD_ERR_NULL_POINTER;
+  if ((reinterpret_cast<uintptr_t>(workspace) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
+  const LayerWs w = layer_ws(d, dtype);
+  if (workspace_bytes < w.total) return SSD_ERR_WORKSPACE_TOO_SMALL;
+  // every operand is checked before the first launch
+  if ((rc = check_rows3(x_in, x_strides, dtype))) return rc;
+  if ((rc = check_rows3(z, z_strides, dtype))) return rc;
+  if (!dt_in || !dt_strides) return SSD_ERR_NULL_POINTER;
+  for (int k = 0; k < 3; ++k)
+    if (dt_strides[k] < 0) return SSD_ERR_BAD_STRIDE;
+  if ((reinterpret_cast<uintptr_t>(dt_in) % elem_size(dtype)) != 0) return SSD_ERR_MISALIGNED;
+  if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
+  if ((rc = check_vec_operand(cmat, c_strides, 4, dtype))) return rc;
+  if (!y || !y_strides) return SSD_ERR_NULL_POINTER;
+  const int64_t P = d->headdim;
+  const int64_t ys4[4] = {y_strides[0], y_strides[1], y_strides[2] * P, y_strides[2]};
+  if ((rc = check_output(y, ys4, dtype))) return rc;
+
+  char* ws = static_cast<char*>(workspace);
+  void* x_out = ws + w.xo;
+  float* dt_out = reinterpret_cast<float*>(ws + w.dto);
+  char* core = ws + w.core;
+  const hipStream_t s = (hipStream_t)stream;
+  if ((rc = launch_layer_prep(d, dtype, prm, x_in, x_strides, dt_in, dt_strides, x_out, dt_out,
+                              reinterpret_cast<float*>(core + w.cw.acs), reinterpret_cast<float*>(core + w.cw.decay),
+                              s)))
+    return rc;
+  const int64_t h = d->nheads, L = d->seqlen;
+  const int64_t xs4[4] = {L * h * P, h * P, P, 1};
+  const int64_t dts[3] = {L * h, h, 1};
+  ssd_epilogue epi;
+  epi.D = prm->D;
+  epi.z = z;
+  epi.z_strides[0] = z_strides[0];
+  epi.z_strides[1] = z_strides[1];
+  epi.z_strides[2] = P * z_strides[2];
+  epi.z_strides[3] = z_strides[2];
+  return run_core(d, dtype, x_out, xs4, bmat, b_strides, cmat, c_strides, dt_out, dts, nullptr, y, ys4, nullptr, core,
+                  w.cw, SSD_DTYPE_F32, &epi, s);
 }
 
 }  // extern "C"

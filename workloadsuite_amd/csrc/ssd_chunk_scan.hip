@@ -27,7 +27,8 @@
 //     by selection so positive log-decays above the diagonal cannot overflow
 //     into inf*0) are applied and the values rounded to the input type.
 //     Fully masked 16x16 blocks are skipped.
-//   * y rows are written once, in the input dtype.
+//   * y rows are written once, in the input dtype; the layer's skip D x and
+//     gate silu(z) (MR:116-118), when given, are applied in float32 first.
 // Workgroup ids are remapped so the heads of one chunk run on one XCD.
 #include "ssd_device.h"
 #include "ssd_launch.h"
@@ -195,15 +196,26 @@ __global__ __launch_bounds__(256, 2) void chunk_scan_kernel(ChunkScanArgs p) {
     }
   }
 
-  // ---- write y[l, p] ----
+  // ---- write y[l, p], with the layer's skip and gate (MR:116-118) when given ----
+  const float dsk = p.dskip ? p.dskip[h] : 0.f;
+  const T* zg = p.z ? reinterpret_cast<const T*>(p.z) + b * p.szb + l0 * p.szl + h * p.szh : nullptr;
 #pragma unroll
   for (int r = 0; r < RT; ++r) {
     const int t = wave + 4 * r;
 #pragma unroll
     for (int jj = 0; jj < 4; ++jj) {
-      T* yrow = yg + (int64_t)(16 * t + 4 * g + jj) * p.syl;
+      const int64_t row = 16 * t + 4 * g + jj;
+      T* yrow = yg + row * p.syl;
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt) yrow[16 * pt + i] = from_f32<T>(acc[r][pt][jj]);
+      for (int pt = 0; pt < 4; ++pt) {
+        float v = acc[r][pt][jj];
+        if (p.dskip) v += dsk * to_f32<T>(xg[row * p.sxl + 16 * pt + i]);
+        if (zg) {
+          const float zv = to_f32<T>(zg[row * p.szl + 16 * pt + i]);
+          v *= zv / (1.f + expf(-zv));
+        }
+        yrow[16 * pt + i] = from_f32<T>(v);
+      }
     }
   }
 }

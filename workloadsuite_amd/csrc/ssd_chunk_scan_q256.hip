@@ -42,6 +42,11 @@
 //
 // Traffic per item: x 32 KB + S_in 32 KB (f32) + Acs 1 KB read, y 32 KB
 // written; B and C per group from L2.  HBM bound at this shape.
+//
+// Layer epilogue (EPI, with dt and chunk_prep's operands): y = (y + D[h] x)
+// * silu(z) (MR:116-118) before y's one rounding.  D x reads x from the
+// item's LDS block; z (32 KB more per item) is loaded into registers once the
+// off-diagonal part is done, in the layout of the y stores.
 #include <climits>
 #include <cstdint>
 #include <type_traits>
@@ -75,12 +80,30 @@ struct ScanArgs32 {
   void* y;
   const float* cbf;  // chunk_prep's CB^T fragments, or null
   int presplit;      // f32 S_in already stored as [hi x8 | lo x8] pairs
-  int sxb, sxl, sxh, sbb, sbl, sbg, scb, scl, scg, sdb, sdl, sdh, syb, syl, syh;
+  const float* dskip;  // epilogue: skip weights [h], or null
+  const void* z;       // epilogue: gate [b, L, h, P], or null
+  int sxb, sxl, sxh, sbb, sbl, sbg, scb, scl, scg, sdb, sdl, sdh, syb, syl, syh, szb, szl, szh;
   int batch, nchunks, nheads, ngroups, dstate;
 };
 
 struct Item {
   int b, c, h, grp;
+};
+
+// CB^T blocks of one 32-token s block (two 16x16 sub-tiles st) as MFMA D
+// fragments: f32, or rounded to T where the registers are needed elsewhere
+// (the epilogue variant's z values).
+template <typename T, bool NARROW>
+struct CbStep {
+  f32x4 v[2];
+  __device__ __forceinline__ void set(int st, f32x4 d) { v[st] = d; }
+  __device__ __forceinline__ f32x4 get(int st) const { return v[st]; }
+};
+template <typename T>
+struct CbStep<T, true> {
+  vec4<T> v[2];
+  __device__ __forceinline__ void set(int st, f32x4 d) { v[st] = __builtin_convertvector(d, vec4<T>); }
+  __device__ __forceinline__ f32x4 get(int st) const { return __builtin_convertvector(v[st], f32x4); }
 };
 
 __device__ __forceinline__ Item item_of(const ScanArgs32& p, int it) {
@@ -93,7 +116,7 @@ __device__ __forceinline__ Item item_of(const ScanArgs32& p, int it) {
   return r;
 }
 
-template <typename T, typename S, int NK, bool HAS_DT, bool PREP>
+template <typename T, typename S, int NK, bool HAS_DT, bool PREP, bool EPI>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void chunk_scan_q256_kernel(ScanArgs32 p) {
   constexpr int N = 32 * NK;                      // dstate (64 or 128)
@@ -260,7 +283,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
 
   // ---- per-group registers: C fragments of both tiles and their CB^T blocks ----
   frag8<T> cf[2][NK];
-  f32x4 cbc[kNPair][2];
+  CbStep<T, EPI> cbc[kNPair];
   auto load_group = [&](int it) __attribute__((always_inline)) {
     int lane_o = lane;
     asm volatile("" : "+v"(lane_o));
@@ -281,7 +304,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
 #pragma unroll
       for (int k = 0; k < kNPair; ++k)
 #pragma unroll
-        for (int st = 0; st < 2; ++st) cbc[k][st] = cb[(k * 2 + st) * 64];
+        for (int st = 0; st < 2; ++st) cbc[k].set(st, cb[(k * 2 + st) * 64]);
       return;
     }
     // One 32-token s block (two 16x16 sub-tiles) per step; every row lies in
@@ -308,7 +331,8 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
         for (int kc = 0; kc < NK; ++kc) d = mma(bfr[st][kc], cfx[kc], d);
         const bool live = 2 * sb + st <= t;
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) cbc[k][st][jj] = live ? d[jj] : 0.f;
+        for (int jj = 0; jj < 4; ++jj) d[jj] = live ? d[jj] : 0.f;
+        cbc[k].set(st, d);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
@@ -320,8 +344,13 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   // block, so its x^T fragments and G factors are read once and feed two
   // independent MFMA chains.
   vec4<T> ypk[2][4];
+  // With the layer's epilogue: y in f32 until the gate, and the gate's z
+  // values of the item (loaded once the off-diagonal part is done, in the
+  // layout store_y writes y in).
+  f32x4 yf[2][4];
+  frag8<T> zv[2][2];
   // off_step(pt) runs before off-diagonal step pt.
-  auto compute = [&](int b, auto off_step) __attribute__((always_inline)) {
+  auto compute = [&](int b, const Item& r, auto off_step) __attribute__((always_inline)) {
     const T* xb = xr[b];
     const unsigned char* sbuf = sr[b];
     const float* ab = wt[wave][0];
@@ -362,10 +391,23 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
 #pragma unroll
       for (int pt = 0; pt < 4; ++pt) acc[s2][pt] *= e;
     }
+    if constexpr (EPI) {
+      if (p.z) {
+        const T* zg = reinterpret_cast<const T*>(p.z) + (int64_t)r.b * p.szb + ((int64_t)r.c * kQ) * p.szl +
+                      (int64_t)r.h * p.szh + ycol;
+#pragma unroll
+        for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+          for (int pp = 0; pp < 2; ++pp)
+            zv[s2][pp] = load8<T>(zg + (int64_t)(16 * (s2 ? tb : ta) + i) * p.szl + 32 * pp);
+      }
+    }
 
     // weighted CB^T block of one tile and s block as an MFMA operand; only
     // the block that crosses the diagonal needs the causal mask.
-    auto weights = [&](int s2, int sb, const f32x4* cb, bool on_diag, const f32x4* gs) __attribute__((always_inline)) {
+    auto weights = [&](int s2, int sb, const CbStep<T, EPI>& cbs, bool on_diag, const f32x4* gs)
+                       __attribute__((always_inline)) {
+      const f32x4 cb[2] = {cbs.get(0), cbs.get(1)};
       frag8<T> af;
       if (on_diag) {
         // The causal-mask predicates depend only on the lane: from an opaque
@@ -440,12 +482,34 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (EPI) {
+      // skip term D x[l, p], x from this item's LDS block (row l, piece
+      // 2 pt + g / 2 at its swizzled slot, half g % 2)
+      if (p.dskip) {
+        const float dsk = p.dskip[r.h];
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2)
+        for (int s2 = 0; s2 < 2; ++s2) {
+          const int l = 16 * (s2 ? tb : ta) + i;
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt)
+          for (int pt = 0; pt < 4; ++pt) {
+            const vec4<T> xv = load4<T>(xb + l * kP + 8 * ((2 * pt + (g >> 1)) ^ (l & 7)) + 4 * (g & 1));
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) ypk[s2][pt][jj] = from_f32<T>(acc[s2][pt][jj]);
+            for (int jj = 0; jj < 4; ++jj) acc[s2][pt][jj] += dsk * to_f32<T>(xv[jj]);
+          }
+        }
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) yf[s2][pt] = acc[s2][pt];
+    } else {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2)
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) ypk[s2][pt][jj] = from_f32<T>(acc[s2][pt][jj]);
+    }
   };
 
   // y of item r from ypk: lane rows g, g ^ 1 swap halves of the column-tile
@@ -457,6 +521,32 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
 #pragma unroll
     for (int s2 = 0; s2 < 2; ++s2) {
       T* yrow = yg + (int64_t)(16 * (s2 ? tb : ta) + i) * p.syl + ycol;
+      if constexpr (EPI) {
+        // the same exchange on f32 values, then the gate, then one rounding
+#pragma unroll
+        for (int pp = 0; pp < 2; ++pp) {
+          // one named swap per word (a loop over the words, assigning vector
+          // elements, lost all but the first swap in compilation)
+          const u32x4 a = __builtin_bit_cast(u32x4, yf[s2][2 * pp]);
+          const u32x4 c = __builtin_bit_cast(u32x4, yf[s2][2 * pp + 1]);
+          const auto w0 = __builtin_amdgcn_permlane16_swap(a[0], c[0], false, false);
+          const auto w1 = __builtin_amdgcn_permlane16_swap(a[1], c[1], false, false);
+          const auto w2 = __builtin_amdgcn_permlane16_swap(a[2], c[2], false, false);
+          const auto w3 = __builtin_amdgcn_permlane16_swap(a[3], c[3], false, false);
+          f32x8 v;
+          v.lo = __builtin_bit_cast(f32x4, u32x4{w0[0], w1[0], w2[0], w3[0]});
+          v.hi = __builtin_bit_cast(f32x4, u32x4{w0[1], w1[1], w2[1], w3[1]});
+          if (p.z) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+              const float zf = to_f32<T>(zv[s2][pp][k]);
+              v[k] *= zf * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-kLog2e * zf));
+            }
+          }
+          store8<T>(yrow + 32 * pp, __builtin_convertvector(v, frag8<T>));
+        }
+        continue;
+      }
 #pragma unroll
       for (int pp = 0; pp < 2; ++pp) {
         const u32x2 a = __builtin_bit_cast(u32x2, ypk[s2][2 * pp]);
@@ -489,7 +579,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     const int bc = (it - it0) & 1, bn = bc ^ 1;
     const bool has_next = it + 1 < it1;
     const Item nxt = has_next ? item_of(p, it + 1) : cur;
-    compute(bc, [&](int pt) __attribute__((always_inline)) {
+    compute(bc, cur, [&](int pt) __attribute__((always_inline)) {
       if (has_next) issue_copy_part(nxt, bn, pt);
     });
     store_y(cur);
@@ -526,6 +616,9 @@ ScanArgs32 narrow(const ChunkScanArgs& a) {
   n.y = a.y;
   n.cbf = a.cbf;
   n.presplit = a.presplit ? 1 : 0;
+  n.dskip = a.dskip;
+  n.z = a.z;
+  n.szb = (int)a.szb, n.szl = (int)a.szl, n.szh = (int)a.szh;
   n.sxb = (int)a.sxb, n.sxl = (int)a.sxl, n.sxh = (int)a.sxh;
   n.sbb = (int)a.sbb, n.sbl = (int)a.sbl, n.sbg = (int)a.sbg;
   n.scb = (int)a.scb, n.scl = (int)a.scl, n.scg = (int)a.scg;
@@ -537,8 +630,13 @@ ScanArgs32 narrow(const ChunkScanArgs& a) {
 
 template <typename T, typename S, int NK>
 hipError_t launch_nk(const ChunkScanArgs& a, hipStream_t stream) {
-  auto kern = a.dt ? (a.cbf ? chunk_scan_q256_kernel<T, S, NK, true, true> : chunk_scan_q256_kernel<T, S, NK, true, false>)
-                   : (a.cbf ? chunk_scan_q256_kernel<T, S, NK, false, true> : chunk_scan_q256_kernel<T, S, NK, false, false>);
+  // the epilogue variant exists for the layer's path only (dt and prep given)
+  const bool epi = a.dskip || a.z;
+  auto kern = epi ? chunk_scan_q256_kernel<T, S, NK, true, true, true>
+              : a.dt ? (a.cbf ? chunk_scan_q256_kernel<T, S, NK, true, true, false>
+                              : chunk_scan_q256_kernel<T, S, NK, true, false, false>)
+                     : (a.cbf ? chunk_scan_q256_kernel<T, S, NK, false, true, false>
+                              : chunk_scan_q256_kernel<T, S, NK, false, false, false>);
   const int items = a.batch * a.nchunks * a.nheads;
   const int grid = persistent_grid(kern, kThreads, items);
   kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(narrow(a));
@@ -559,10 +657,15 @@ hipError_t launch_ts(const ChunkScanArgs& a, hipStream_t stream) {
 bool chunk_scan_persistent_supported(const ChunkScanArgs& a, int dtype) {
   // dstate 16 / 32 stay on the generic kernel (this one spills registers there).
   for (int64_t st : {a.sxb, a.sxl, a.sxh, a.sbb, a.sbl, a.sbg, a.scb, a.scl, a.scg, a.sdb, a.sdl, a.sdh, a.syb,
-                     a.syl, a.syh})
+                     a.syl, a.syh, a.szb, a.szl, a.szh})
     if (!fits_i32(st)) return false;
-  // y is written 16 bytes per lane
+  // y is written (and z read) 16 bytes per lane
   if (reinterpret_cast<uintptr_t>(a.y) % 16 != 0 || a.syb % 8 != 0 || a.syl % 8 != 0 || a.syh % 8 != 0) return false;
+  if (a.dskip || a.z) {
+    if (!a.dt || !a.cbf) return false;
+    if (a.z && (reinterpret_cast<uintptr_t>(a.z) % 16 != 0 || a.szb % 8 != 0 || a.szl % 8 != 0 || a.szh % 8 != 0))
+      return false;
+  }
   return a.chunk == kQ && (a.dstate == 64 || a.dstate == 128) &&
          (dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16);
 }

@@ -13,8 +13,13 @@
 // lane totals (DPP/permute shuffles, log2(64) steps) gives each lane its
 // offset.  HBM traffic is one read of A and one write of Acs: memory bound,
 // about 8 bytes per token and head.
+//
+// Layer variant (RAW = true): the tile is formed from in_proj's raw dt
+// instead of A (MR:94, 102-103): dt = softplus(dt_raw + dt_bias[h]) in
+// float32 (written out, [b, L, h], for K2 / K4), A_dt = -exp(A_log[h]) dt.
 #include "ssd_device.h"
 #include "ssd_launch.h"
+#include "../../include/ssd.h"
 
 namespace ssd {
 
@@ -31,7 +36,11 @@ __device__ __forceinline__ float wave_inclusive_scan(float v, int lane) {
   return v;
 }
 
-template <int Q>
+// log(1 + e^v), and v itself above 20 (torch.nn.functional.softplus's
+// default threshold, as MR:94 calls it)
+__device__ __forceinline__ float softplus(float v) { return v > 20.f ? v : log1pf(expf(v)); }
+
+template <int Q, typename R, bool RAW>
 __global__ __launch_bounds__(256) void chunk_cumsum_kernel(CumsumArgs p) {
   constexpr int PER = Q / kWave;  // tokens per lane
   __shared__ float tile[kHeadTile][Q + 1];
@@ -45,10 +54,26 @@ __global__ __launch_bounds__(256) void chunk_cumsum_kernel(CumsumArgs p) {
   const int h0 = ht * kHeadTile;
   const int nh = min(kHeadTile, p.nheads - h0);
 
-  const float* src = p.a + (int64_t)b * p.sab + (int64_t)c * Q * p.sal + (int64_t)h0 * p.sah;
-  for (int e = threadIdx.x; e < Q * kHeadTile; e += 256) {
-    const int l = e / kHeadTile, hh = e % kHeadTile;
-    tile[hh][l] = hh < nh ? src[(int64_t)l * p.sal + (int64_t)hh * p.sah] : 0.f;
+  if constexpr (RAW) {
+    const R* src = static_cast<const R*>(p.dt_raw) + (int64_t)b * p.srb + (int64_t)c * Q * p.srl + (int64_t)h0 * p.srh;
+    const R* bias = static_cast<const R*>(p.dt_bias) + h0;
+    float* dto = p.dt_out + ((int64_t)b * p.nchunks * Q + (int64_t)c * Q) * p.nheads + h0;
+    for (int e = threadIdx.x; e < Q * kHeadTile; e += 256) {
+      const int l = e / kHeadTile, hh = e % kHeadTile;
+      float a = 0.f;
+      if (hh < nh) {
+        const float dt = softplus(to_f32<R>(src[(int64_t)l * p.srl + (int64_t)hh * p.srh]) + to_f32<R>(bias[hh]));
+        dto[(int64_t)l * p.nheads + hh] = dt;
+        a = -expf(p.a_log[h0 + hh]) * dt;
+      }
+      tile[hh][l] = a;
+    }
+  } else {
+    const float* src = p.a + (int64_t)b * p.sab + (int64_t)c * Q * p.sal + (int64_t)h0 * p.sah;
+    for (int e = threadIdx.x; e < Q * kHeadTile; e += 256) {
+      const int l = e / kHeadTile, hh = e % kHeadTile;
+      tile[hh][l] = hh < nh ? src[(int64_t)l * p.sal + (int64_t)hh * p.sah] : 0.f;
+    }
   }
   __syncthreads();
 
@@ -72,18 +97,29 @@ __global__ __launch_bounds__(256) void chunk_cumsum_kernel(CumsumArgs p) {
   }
 }
 
-}  // namespace
-
-hipError_t launch_chunk_cumsum(const CumsumArgs& a, hipStream_t stream) {
+template <typename R, bool RAW>
+hipError_t launch_q(const CumsumArgs& a, hipStream_t stream) {
   const int htiles = (a.nheads + kHeadTile - 1) / kHeadTile;
   const dim3 grid((unsigned)((int64_t)a.batch * a.nchunks * htiles));
   switch (a.chunk) {
-    case 64: chunk_cumsum_kernel<64><<<grid, 256, 0, stream>>>(a); break;
-    case 128: chunk_cumsum_kernel<128><<<grid, 256, 0, stream>>>(a); break;
-    case 256: chunk_cumsum_kernel<256><<<grid, 256, 0, stream>>>(a); break;
+    case 64: chunk_cumsum_kernel<64, R, RAW><<<grid, 256, 0, stream>>>(a); break;
+    case 128: chunk_cumsum_kernel<128, R, RAW><<<grid, 256, 0, stream>>>(a); break;
+    case 256: chunk_cumsum_kernel<256, R, RAW><<<grid, 256, 0, stream>>>(a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_chunk_cumsum(const CumsumArgs& a, hipStream_t stream) {
+  if (!a.dt_raw) return launch_q<float, false>(a, stream);
+  switch (a.raw_dtype) {
+    case SSD_DTYPE_F32: return launch_q<float, true>(a, stream);
+    case SSD_DTYPE_BF16: return launch_q<bf16, true>(a, stream);
+    case SSD_DTYPE_F16: return launch_q<f16, true>(a, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace ssd

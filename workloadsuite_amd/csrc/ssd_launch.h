@@ -15,7 +15,29 @@ struct CumsumArgs {
   float* acs;             // [b, h, c, Q]
   float* decay;           // [b, h, c]
   int batch, nchunks, nheads, chunk;
+  // Optional (the layer's prep): a = -exp(a_log[h]) softplus(dt_raw + dt_bias[h])
+  // is formed here, and that dt written to dt_out ([b, L, h] f32, contiguous);
+  // `a` is then unused.  dt_raw and dt_bias are of raw_dtype.
+  const void* dt_raw = nullptr;
+  int64_t srb = 0, srl = 0, srh = 0;
+  const void* dt_bias = nullptr;
+  const float* a_log = nullptr;
+  float* dt_out = nullptr;
+  int raw_dtype = 0;
 };
+
+// Causal depthwise conv1d of width kwidth over the sequence, plus bias, then
+// SiLU (ssd_layer_prep.hip): y [b, L, channels] contiguous from x [b, L,
+// channels] (unit channel stride); w [channels, kwidth], bias [channels] or null.
+struct ConvArgs {
+  const void* x;
+  int64_t sxb, sxl;
+  const void* w;
+  const void* bias;
+  void* y;
+  int batch, seqlen, channels, kwidth;
+};
+hipError_t launch_conv_silu(const ConvArgs& a, int dtype, hipStream_t stream);
 
 struct ChunkStateArgs {
   const void* x;
@@ -57,6 +79,10 @@ struct ChunkScanArgs {
   int batch, nchunks, nheads, ngroups, dstate, chunk;
   const float* cbf = nullptr;  // optional chunk_prep CB^T fragments (persistent kernel)
   bool presplit = false;       // f32 states already split by state_passing (split_dtype)
+  // optional epilogue: y = (y + dskip[h] x) * silu(z)
+  const float* dskip = nullptr;  // [h]
+  const void* z = nullptr;       // [b, L, h, P], unit stride over P
+  int64_t szb = 0, szl = 0, szh = 0;
 };
 
 // K0 -- per-(b, c, group) operands of the chunk-256 persistent kernels

@@ -4,28 +4,29 @@ constructor signatures, parameter names, shapes and dtypes (MR:13-66,
 165-196), so a reference ``state_dict`` loads unchanged and the reference
 harness (bench.py:104-115, 217-233) runs this module as it runs MR.
 
-The SSD core (MR:112, ``_ssd_core``, MR:123-162) runs in libssd's HIP kernels
-through ``ssd_forward``: B and C are passed per group (no GQA ``repeat``,
+Everything between the two projections (MR:76-118) is one libssd call,
+``ssd_layer``: the causal depthwise conv + SiLU, softplus(dt + dt_bias) and
+A_dt = -exp(A_log) dt in two HIP launches (MR:83-103), then the SSD core
+(MR:112, ``_ssd_core``, MR:123-162), whose last kernel applies the skip
+``+ x D`` and the gate ``* silu(z)`` (MR:116-118) before its single write of y.
+B and C are read per group from in_proj's output (no GQA ``repeat``,
 MR:97-99), the chunking rearranges (MR:105-110, 115) disappear because the
 kernels take ``[b, L, ...]`` tensors with strides, and dt scales x inside the
-kernels in float32 (MR:144 multiplies in float16).  The glue around the core
--- RMSNorm, the two projections, the depthwise causal conv, SiLU, softplus,
-the skip and the gate (MR:70-121) -- stays on PyTorch-ROCm (hipBLASLt/rocBLAS
-GEMMs and elementwise kernels), in MR's float16.
+kernels in float32 (MR:144 multiplies in float16).  RMSNorm and the two
+projections stay on PyTorch-ROCm (hipBLASLt/rocBLAS GEMMs), in MR's float16.
 
-Differences from MR a caller can observe: the core accumulates in float32 and
-keeps the per-chunk states in float32 (MR rounds intermediates to float16 at
-MR:145, 148, 155, 160), so outputs agree with MR to float16 rounding, not bit
-for bit.
+Differences from MR a caller can observe: the kernels accumulate and activate
+in float32 and keep dt and the per-chunk states in float32 (MR rounds
+intermediates to float16 at MR:85-86, 94, 145, 148, 155, 160 and 116-118), so
+outputs agree with MR to float16 rounding, not bit for bit.
 """
 
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 
-from .ssd import ssd_forward
+from .ssd import ssd_layer
 
 __all__ = ["SSDLayer", "Model", "get_inputs", "get_init_inputs"]
 
@@ -61,17 +62,11 @@ class SSDLayer(nn.Module):
         b, L, _ = u.shape
         if L % self.block_len != 0:
             raise ValueError(f"seqlen {L} is not a multiple of block_len {self.block_len}")
-        h, P, g, N = self.n_heads, self.d_head, self.n_groups, self.d_state
+        h, g, N = self.n_heads, self.n_groups, self.d_state
         zxbcdt = self.in_proj(self.norm(u))
         x, z, B, C, dt = torch.split(zxbcdt, [self.d_inner, self.d_inner, g * N, g * N, h], dim=-1)
-        # causal depthwise conv over time, then SiLU; [b, L, d_inner] with unit stride on d
-        x = F.silu(self.conv1d(x.transpose(1, 2))[..., :L]).transpose(1, 2).contiguous()
-        X = x.view(b, L, h, P)
-        dt = F.softplus(dt + self.dt_bias)
-        A_dt = -torch.exp(self.A_log) * dt.float()
-        Y = ssd_forward(X, A_dt, B.view(b, L, g, N), C.view(b, L, g, N), self.block_len, dt=dt.float())
-        Y = Y + X * self.D.view(1, 1, -1, 1)
-        Y = Y.reshape(b, L, self.d_inner) * F.silu(z)
+        Y = ssd_layer(x, z, B.view(b, L, g, N), C.view(b, L, g, N), dt, self.conv1d.weight, self.conv1d.bias,
+                      self.dt_bias, self.A_log, self.D, self.block_len, h)
         return self.out_proj(Y)
 
 

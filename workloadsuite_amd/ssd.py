@@ -42,6 +42,8 @@ __all__ = [
     "state_passing",
     "state_passing_",
     "chunk_scan",
+    "layer_prep",
+    "ssd_layer",
     "workspace_bytes",
     "SSDError",
 ]
@@ -295,10 +297,37 @@ def state_passing_(states, chunk_decay, initial_states=None, final_states=None, 
     return states
 
 
-def chunk_scan(X, B, C, Acs, states, dt=None, prep=None, split=False):
+def _epilogue(X, D, z, dev):
+    """The skip / gate epilogue struct (or None) and the tensors it points into."""
+    if D is None and z is None:
+        return None, ()
+    epi = _lib.SSDEpilogue()
+    keep = []
+    if D is not None:
+        D = _f32_contig(D.reshape(-1))
+        if D.device != dev or D.numel() != X.shape[2]:
+            raise ValueError(f"D must be [{X.shape[2]}] on {dev}")
+        epi.D = D.data_ptr()
+        keep.append(D)
+    if z is not None:
+        if z.shape != X.shape or z.dtype != X.dtype or z.device != dev:
+            raise ValueError(f"z must match X: {tuple(X.shape)} {X.dtype} on {dev}")
+        z = z.detach()
+        if z.stride(-1) != 1 or any(st < 0 for st in z.stride()):
+            z = z.contiguous()
+        epi.z = z.data_ptr()
+        for k in range(4):
+            epi.z_strides[k] = z.stride(k)
+        keep.append(z)
+    return epi, keep
+
+
+def chunk_scan(X, B, C, Acs, states, dt=None, prep=None, split=False, D=None, z=None):
     """K4: Y [b, L, h, P] from the states entering each chunk (MR:139-145, 160-162).
     ``prep``: chunk_prep(B, C, Q) or None.  ``split``: ``states`` holds
-    state_passing(..., split=X.dtype)'s (hi, lo) pairs."""
+    state_passing(..., split=X.dtype)'s (hi, lo) pairs.  ``D`` [h] and / or
+    ``z`` (X's shape and dtype): the layer's skip and gate fused into the write,
+    Y = (Y + D x) * silu(z) (MR:116-118)."""
     b, L, h, P = X.shape
     g, N = B.shape[2], B.shape[3]
     Q = Acs.shape[-1]
@@ -311,9 +340,108 @@ def chunk_scan(X, B, C, Acs, states, dt=None, prep=None, split=False):
     if not S.is_contiguous():
         S = S.contiguous()
     Y = torch.empty((b, L, h, P), dtype=X.dtype, device=dev)
+    epi, _keep = _epilogue(X, D, z, dev)
     _lib.check(_lib.load().ssd_chunk_scan(
         ctypes.byref(d), _DTYPES[X.dtype], _ptr(X), _lib.strides(X), _ptr(Bm), _lib.strides(Bm),
         _ptr(Cm), _lib.strides(Cm), _ptr(dt), _lib.strides(dt) if dt is not None else None,
         _ptr(Acs), _ptr(S), _SPLIT_STATES[X.dtype] if split else _STATE_DTYPES[S.dtype], _ptr(Y),
-        _lib.strides(Y), _ptr(prep), _stream(dev)))
+        _lib.strides(Y), _ptr(prep), ctypes.byref(epi) if epi is not None else None, _stream(dev)))
     return Y
+
+
+# ---------------------------------------------------------------------------
+# the layer around the core (SSDLayer.forward, MR:76-118)
+# ---------------------------------------------------------------------------
+
+def _layer_params(conv_weight, conv_bias, dt_bias, A_log, D, d_inner, nheads, dtype, dev):
+    k = conv_weight.shape[-1]
+    if conv_weight.numel() != d_inner * k:
+        raise ValueError(f"conv weight must be [{d_inner}, 1, k], got {tuple(conv_weight.shape)}")
+    w = conv_weight.detach().reshape(d_inner, k).to(dtype).contiguous()
+    bias = None if conv_bias is None else conv_bias.detach().reshape(d_inner).to(dtype).contiguous()
+    dtb = dt_bias.detach().reshape(nheads).to(dtype).contiguous()
+    alog = _f32_contig(A_log.reshape(nheads))
+    Dv = None if D is None else _f32_contig(D.reshape(nheads))
+    for t in (w, bias, dtb, alog, Dv):
+        if t is not None and t.device != dev:
+            raise ValueError(f"layer parameters must be on {dev}, got {t.device}")
+    prm = _lib.SSDLayerParams(k, w.data_ptr(), 0 if bias is None else bias.data_ptr(), dtb.data_ptr(),
+                              alog.data_ptr(), 0 if Dv is None else Dv.data_ptr())
+    return prm, (w, bias, dtb, alog, Dv)
+
+
+def _rows3(t):
+    t = t.detach()
+    if t.stride(-1) != 1 or any(st < 0 for st in t.stride()):
+        t = t.contiguous()
+    return t
+
+
+def layer_prep(x, dt, conv_weight, conv_bias, dt_bias, A_log, chunk_size, nheads, ngroups=1, dstate=64):
+    """Pre-SSD prep (MR:83-103) in two HIP launches.
+
+    ``x`` [b, L, h*P] and ``dt`` [b, L, h] are in_proj's output slices (any
+    strides, unit inner stride).  Returns ``(X, dt, Acs, chunk_decay)``: X =
+    silu(causal depthwise conv1d(x) + bias) as [b, L, h, P] in x's dtype, dt =
+    softplus(dt + dt_bias) in float32, and K1's cumsum of A dt with A =
+    -exp(A_log).  ``ngroups`` / ``dstate`` only enter the shape validation."""
+    b, L, d_inner = x.shape
+    if dt.shape != (b, L, nheads) or d_inner % nheads != 0:
+        raise ValueError(f"dt must be {(b, L, nheads)} and d_inner a multiple of nheads")
+    P = d_inner // nheads
+    if x.dtype not in _DTYPES or dt.dtype != x.dtype:
+        raise ValueError(f"x and dt must share a supported dtype, got {x.dtype} and {dt.dtype}")
+    if chunk_size < 1 or L % chunk_size != 0:
+        raise ValueError(f"seqlen {L} is not a multiple of chunk size {chunk_size}")
+    dev = _device_check(x, dt, conv_weight, dt_bias, A_log)
+    d = _dims(b, L, nheads, P, dstate, ngroups, chunk_size)
+    prm, _keep = _layer_params(conv_weight, conv_bias, dt_bias, A_log, None, d_inner, nheads, x.dtype, dev)
+    x, dt = _rows3(x), _rows3(dt)
+    X = torch.empty((b, L, nheads, P), dtype=x.dtype, device=dev)
+    dto = torch.empty((b, L, nheads), dtype=torch.float32, device=dev)
+    c = L // chunk_size
+    Acs = torch.empty((b, nheads, c, chunk_size), dtype=torch.float32, device=dev)
+    dec = torch.empty((b, nheads, c), dtype=torch.float32, device=dev)
+    _lib.check(_lib.load().ssd_layer_prep(
+        ctypes.byref(d), _DTYPES[x.dtype], ctypes.byref(prm), _ptr(x), _lib.strides(x), _ptr(dt),
+        _lib.strides(dt), _ptr(X), _ptr(dto), _ptr(Acs), _ptr(dec), _stream(dev)))
+    return X, dto, Acs, dec
+
+
+def ssd_layer(x, z, B, C, dt, conv_weight, conv_bias, dt_bias, A_log, D, chunk_size, nheads):
+    """SSDLayer.forward between its projections (MR:76-118), one C-ABI call:
+    pre-SSD prep, the SSD core and the skip + gate fused into its output.
+
+    ``x``, ``z`` [b, L, h*P]; ``B``, ``C`` [b, L, g, N]; ``dt`` [b, L, h] --
+    in_proj's output slices, all of one dtype (MR: float16).  ``conv_weight``
+    [h*P, 1, k], ``conv_bias`` [h*P] or None, ``dt_bias`` [h], ``A_log`` [h],
+    ``D`` [h] or None: MR's parameters.  Returns y [b, L, h*P] in x's dtype,
+    out_proj's input."""
+    b, L, d_inner = x.shape
+    if z.shape != x.shape or dt.shape != (b, L, nheads) or d_inner % nheads != 0:
+        raise ValueError("x and z must be [b, L, h*P] and dt [b, L, h]")
+    if B.dim() != 4 or B.shape[:2] != (b, L) or C.shape != B.shape:
+        raise ValueError(f"B and C must be [b, L, g, N], got {tuple(B.shape)} and {tuple(C.shape)}")
+    P = d_inner // nheads
+    g, N = B.shape[2], B.shape[3]
+    if nheads % g != 0:
+        raise ValueError("n_heads must be divisible by n_groups")
+    if chunk_size < 1 or L % chunk_size != 0:
+        raise ValueError(f"seqlen {L} is not a multiple of chunk size {chunk_size}")
+    dtype = x.dtype
+    if dtype not in _DTYPES or any(t.dtype != dtype for t in (z, B, C, dt)):
+        raise ValueError("x, z, B, C and dt must share a supported dtype")
+    dev = _device_check(x, z, B, C, dt, conv_weight, dt_bias, A_log)
+    d = _dims(b, L, nheads, P, N, g, chunk_size)
+    prm, _keep = _layer_params(conv_weight, conv_bias, dt_bias, A_log, D, d_inner, nheads, dtype, dev)
+    x, z, dt = _rows3(x), _rows3(z), _rows3(dt)
+    Bm, Cm = _vec_operand(B.detach()), _vec_operand(C.detach())
+    lib = _lib.load()
+    nbytes = lib.ssd_layer_workspace_bytes(ctypes.byref(d), _DTYPES[dtype])
+    ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=dev)
+    y = torch.empty((b, L, d_inner), dtype=dtype, device=dev)
+    _lib.check(lib.ssd_layer_forward(
+        ctypes.byref(d), _DTYPES[dtype], ctypes.byref(prm), _ptr(x), _lib.strides(x), _ptr(z), _lib.strides(z),
+        _ptr(Bm), _lib.strides(Bm), _ptr(Cm), _lib.strides(Cm), _ptr(dt), _lib.strides(dt), _ptr(y),
+        _lib.strides(y), _ptr(ws), nbytes, _stream(dev)))
+    return y
