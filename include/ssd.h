@@ -219,7 +219,8 @@ int ssd_layer_prep(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
                    void* stream);
 
 /* Workspace of ssd_layer_forward: x_out, dt_out, then ssd_workspace_bytes
- * (f32 states), each 256-byte aligned; 0 when dims are invalid. */
+ * (f32 states) at the chunk the core runs at, each 256-byte aligned; 0 when
+ * dims are invalid. */
 size_t ssd_layer_workspace_bytes(const ssd_dims* d, int dtype);
 
 /* SSDLayer.forward between its two projections (MR:76-118): from in_proj's
@@ -228,7 +229,11 @@ size_t ssd_layer_workspace_bytes(const ssd_dims* d, int dtype);
  * out_proj's input y [b, L, h*P]:
  *   ssd_layer_prep, then the SSD core (K0, K2, K3, K4 of ssd_forward), with
  *   the skip D x and the gate silu(z) fused into K4's write of y.
- * z_strides / y_strides are over [b, L, h*P]. */
+ * z_strides / y_strides are over [b, L, h*P].  d->chunk is MR's block_len
+ * and only has to divide L: for 16-bit inputs with L % 256 == 0 and dstate
+ * 64 / 128 the core runs at chunk 256, whose result equals every other
+ * chunking's up to rounding (the chunked SSD evaluates one linear recurrence,
+ * MR:152-161) and whose per-chunk states take a quarter of the memory. */
 int ssd_layer_forward(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
                       const void* x_in, const int64_t x_strides[3],
                       const void* z, const int64_t z_strides[3],

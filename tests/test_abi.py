@@ -176,10 +176,17 @@ def test_layer_entry_points_validate_on_the_host():
     bad = (ctypes.c_int64 * 3)(256 * 1000, 1000, 2)
     assert lib.ssd_layer_prep(ctypes.byref(dims), 2, ctypes.byref(prm), fake, bad, fake, s3,
                               fake, fake, fake, fake, None) == -9
-    # workspace: x (f16) and dt (f32) ahead of the core's f32-state workspace
+    # workspace: x (f16) and dt (f32) ahead of the core's f32-state workspace,
+    # which is sized at chunk 256 for 16-bit inputs when L allows it
     n = lib.ssd_layer_workspace_bytes(ctypes.byref(dims), 2)
     tokens = 2 * 256
-    assert n == tokens * 8 * 64 * 2 + tokens * 8 * 4 + lib.ssd_workspace_bytes(ctypes.byref(dims), 0)
+    core = d(chunk=256)
+    assert n == tokens * 8 * 64 * 2 + tokens * 8 * 4 + lib.ssd_workspace_bytes(ctypes.byref(core), 0)
+    f32 = lib.ssd_layer_workspace_bytes(ctypes.byref(dims), 0)
+    assert f32 == tokens * 8 * 64 * 4 + tokens * 8 * 4 + lib.ssd_workspace_bytes(ctypes.byref(dims), 0)
+    odd = d(seqlen=320)
+    assert lib.ssd_layer_workspace_bytes(ctypes.byref(odd), 2) == (
+        2 * 320 * 8 * 64 * 2 + 2 * 320 * 8 * 4 + lib.ssd_workspace_bytes(ctypes.byref(odd), 0))
     ys = (ctypes.c_int64 * 3)(256 * 512, 512, 1)
     fwd = lambda ws, nb: lib.ssd_layer_forward(ctypes.byref(dims), 2, ctypes.byref(prm), fake, s3, fake, s3,  # noqa: E731
                                                fake, bs4, fake, bs4, fake, s3, fake, ys, ws, nb, None)

@@ -150,12 +150,14 @@ def test_chunk_scan_epilogue(dtype, Q, N, use_prep, epi):
 
 
 @pytest.mark.parametrize("dtype", DTYPES)
-@pytest.mark.parametrize("Q,N,g", [(64, 128, 2), (256, 128, 1), (256, 64, 2)])
-def test_ssd_layer_matches_oracle(dtype, Q, N, g):
-    """One C-ABI call from in_proj's output slices to out_proj's input."""
-    say("ssd_layer", dtype, Q, N, g)
+@pytest.mark.parametrize("Q,N,g,L", [(64, 128, 2, 128), (64, 128, 2, 512), (128, 64, 4, 768), (256, 128, 1, 512),
+                                     (256, 64, 2, 512)])
+def test_ssd_layer_matches_oracle(dtype, Q, N, g, L):
+    """One C-ABI call from in_proj's output slices to out_proj's input.  With
+    16-bit inputs and L % 256 == 0 the core runs at chunk 256 whatever the
+    block_len; the oracle evaluates MR's chunking at Q."""
+    say("ssd_layer", dtype, Q, N, g, L)
     h, P = 8, 64
-    L = 2 * Q
     proj, prm = layer_case(dtype, b=2, L=L, h=h, P=P, g=g, N=N)
     x, z, B, C, dt = split(proj, h, P, g, N)
     pd = proj.to(DEV)

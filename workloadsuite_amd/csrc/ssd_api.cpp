@@ -302,6 +302,20 @@ int run_core(const ssd_dims* d, int dtype, const void* x, const int64_t x_stride
 
 // ---- the layer around the core ----
 
+// The chunk length the layer's core runs at.  The chunked SSD's output does
+// not depend on the chunk length (every chunking evaluates the same linear
+// recurrence, MR:152-161); MR's block_len only has to divide L.  With 16-bit
+// inputs chunk 256 runs the persistent kernels and stores a quarter of the
+// per-chunk states of chunk 64 (at MR's shape those states are most of the
+// core's HBM traffic), so the layer uses it whenever L and dstate allow.
+ssd_dims layer_core_dims(const ssd_dims* d, int dtype) {
+  ssd_dims e = *d;
+  if ((dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16) && d->seqlen % 256 == 0 &&
+      (d->dstate == 64 || d->dstate == 128))
+    e.chunk = 256;
+  return e;
+}
+
 struct LayerWs {
   size_t xo, dto, core, total;
   WsLayout cw;
@@ -313,7 +327,8 @@ LayerWs layer_ws(const ssd_dims* d, int dtype) {
   w.xo = 0;
   w.dto = round_up(tokens * d->nheads * d->headdim * elem_size(dtype));
   w.core = w.dto + round_up(tokens * d->nheads * sizeof(float));
-  w.cw = ws_layout(d, SSD_DTYPE_F32);
+  const ssd_dims e = layer_core_dims(d, dtype);
+  w.cw = ws_layout(&e, SSD_DTYPE_F32);
   w.total = w.core + w.cw.total;
   return w;
 }
@@ -624,6 +639,8 @@ int ssd_layer_forward(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
   float* dt_out = reinterpret_cast<float*>(ws + w.dto);
   char* core = ws + w.core;
   const hipStream_t s = (hipStream_t)stream;
+  const ssd_dims e = layer_core_dims(d, dtype);
+  d = &e;
   if ((rc = launch_layer_prep(d, dtype, prm, x_in, x_strides, dt_in, dt_strides, x_out, dt_out,
                               reinterpret_cast<float*>(core + w.cw.acs), reinterpret_cast<float*>(core + w.cw.decay),
                               s)))

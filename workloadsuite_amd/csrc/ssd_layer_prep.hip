@@ -22,8 +22,8 @@ namespace ssd {
 
 namespace {
 
-constexpr int kRun = 32;     // tokens per lane
-constexpr int kBatchRows = 8;  // rows loaded together (independent loads in flight)
+constexpr int kRun = 64;       // tokens per lane
+constexpr int kBatchRows = 8;  // rows per batch; the next batch's loads are in flight during this one's math
 constexpr int kWavesPerBlock = 4;
 
 template <typename T, int V>
@@ -73,14 +73,25 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void conv_silu_kernel(ConvArgs
 
   float w[K][V], bias[V];
   {
+    // the lane's V x K weights are contiguous: 16-byte loads where they fill them
     const T* wg = static_cast<const T*>(p.w) + (int64_t)d0 * K;
     const T* bg = static_cast<const T*>(p.bias);
+    constexpr int WV = 16 / sizeof(T);
+    if constexpr ((V * K) % WV == 0 && V * sizeof(T) == 16) {
 #pragma unroll
-    for (int e = 0; e < V; ++e) {
+      for (int q = 0; q < V * K / WV; ++q) {
+        const Row<T, WV> r = load_row<T, WV>(wg + q * WV);
 #pragma unroll
-      for (int j = 0; j < K; ++j) w[j][e] = to_f32<T>(wg[e * K + j]);
-      bias[e] = bg ? to_f32<T>(bg[d0 + e]) : 0.f;
+        for (int u = 0; u < WV; ++u) w[(q * WV + u) % K][(q * WV + u) / K] = to_f32<T>(r.v[u]);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < V; ++e)
+#pragma unroll
+        for (int j = 0; j < K; ++j) w[j][e] = to_f32<T>(wg[e * K + j]);
     }
+#pragma unroll
+    for (int e = 0; e < V; ++e) bias[e] = bg ? to_f32<T>(bg[d0 + e]) : 0.f;
   }
   const T* xg = static_cast<const T*>(p.x) + (int64_t)b * p.sxb + d0;
   T* yg = static_cast<T*>(p.y) + ((int64_t)b * p.seqlen) * p.channels + d0;
@@ -100,12 +111,19 @@ __global__ __launch_bounds__(64 * kWavesPerBlock) void conv_silu_kernel(ConvArgs
     }
   }
 
-  const int nrows = min(kRun, p.seqlen - l0);  // a multiple of kBatchRows unless L is not
+  const int nrows = min(kRun, p.seqlen - l0);
+  Row<T, V> nxt[kBatchRows];
+  auto load_batch = [&](int t0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < kBatchRows; ++t)
+      if (t0 + t < nrows) nxt[t] = load_row<T, V>(xg + (int64_t)(l0 + t0 + t) * p.sxl);
+  };
+  load_batch(0);
   for (int t0 = 0; t0 < nrows; t0 += kBatchRows) {
     Row<T, V> in[kBatchRows];
 #pragma unroll
-    for (int t = 0; t < kBatchRows; ++t)
-      if (t0 + t < nrows) in[t] = load_row<T, V>(xg + (int64_t)(l0 + t0 + t) * p.sxl);
+    for (int t = 0; t < kBatchRows; ++t) in[t] = nxt[t];
+    if (t0 + kBatchRows < nrows) load_batch(t0 + kBatchRows);
 #pragma unroll
     for (int t = 0; t < kBatchRows; ++t) {
       if (t0 + t >= nrows) break;
@@ -144,13 +162,14 @@ hipError_t launch_tv(const ConvArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// 16-byte vectors when x rows, y rows and the channel count allow them,
-// else one channel per lane.
+// 16-byte vectors when x rows, y rows, the weights and the channel count
+// allow them, else one channel per lane.
 template <typename T>
 hipError_t launch_t(const ConvArgs& a, hipStream_t stream) {
   constexpr int V = 16 / sizeof(T);
   const bool vec = a.channels % V == 0 && (reinterpret_cast<uintptr_t>(a.x) & 15u) == 0 &&
-                   (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0 && (a.sxb * (int64_t)sizeof(T)) % 16 == 0 &&
+                   (reinterpret_cast<uintptr_t>(a.y) & 15u) == 0 && (reinterpret_cast<uintptr_t>(a.w) & 15u) == 0 &&
+                   (a.sxb * (int64_t)sizeof(T)) % 16 == 0 &&
                    (a.sxl * (int64_t)sizeof(T)) % 16 == 0;
   return vec ? launch_tv<T, V>(a, stream) : launch_tv<T, 1>(a, stream);
 }

@@ -12,7 +12,11 @@ A_dt = -exp(A_log) dt in two HIP launches (MR:83-103), then the SSD core
 B and C are read per group from in_proj's output (no GQA ``repeat``,
 MR:97-99), the chunking rearranges (MR:105-110, 115) disappear because the
 kernels take ``[b, L, ...]`` tensors with strides, and dt scales x inside the
-kernels in float32 (MR:144 multiplies in float16).  RMSNorm and the two
+kernels in float32 (MR:144 multiplies in float16).  ``block_len`` keeps MR's
+meaning for validation (it must divide the sequence length); the core itself
+runs at chunk 256 whenever L allows, which gives the same result up to
+rounding (every chunking evaluates the same recurrence) with a quarter of the
+per-chunk state traffic of chunk 64.  RMSNorm and the two
 projections stay on PyTorch-ROCm (hipBLASLt/rocBLAS GEMMs), in MR's float16.
 
 Differences from MR a caller can observe: the kernels accumulate and activate
