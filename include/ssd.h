@@ -189,6 +189,27 @@ int ssd_forward(const ssd_dims* d, int dtype,
                 void* workspace, size_t workspace_bytes, int state_dtype,
                 void* stream);
 
+/* Decode: one token of the recurrence (the per-token form of MR:152-161),
+ * in place on a [b, h, P, N] f32 state such as ssd_forward's final_states:
+ *   state[b,h,p,n] = exp(a[b,h]) state[b,h,p,n] + dt[b,h] x[b,h,p] bmat[b,g,n]
+ *   y[b,h,p]       = sum_n cmat[b,g,n] state[b,h,p,n]
+ * with head h reading group h / (nheads / ngroups), then the optional
+ * epilogue (skip D x, gate silu(z)).  MR has no single-token path; this is the
+ * consumer of the final state it computes (MR:156).  d->seqlen and d->chunk
+ * are not used.  x, y: [b, h, P] of dtype, element strides {batch, head}
+ * (unit stride over P).  bmat, cmat: [b, g, N] of dtype, strides {batch,
+ * group} (unit over N).  a, dt: [b, h] f32 with strides ad_strides {batch,
+ * head}; dt NULL means 1.  state: contiguous, 16-byte aligned.  The
+ * epilogue's z is [b, h, P] with z_strides[0] (batch) and z_strides[2]
+ * (head); z_strides[1] is not used. */
+int ssd_decode_step(const ssd_dims* d, int dtype, float* state,
+                    const void* x, const int64_t x_strides[2],
+                    const void* bmat, const int64_t b_strides[2],
+                    const void* cmat, const int64_t c_strides[2],
+                    const float* a, const float* dt, const int64_t ad_strides[2],
+                    void* y, const int64_t y_strides[2],
+                    const ssd_epilogue* epilogue, void* stream);
+
 /* ---- the layer around the SSD core (SSDLayer.forward, MR:68-121) ---- */
 
 /* Parameters of one layer, as MR's module holds them (MR:41-66).  Device

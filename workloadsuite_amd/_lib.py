@@ -32,6 +32,7 @@ EXPORTS = (
     "ssd_state_passing",
     "ssd_chunk_scan",
     "ssd_forward",
+    "ssd_decode_step",
     "ssd_layer_prep",
     "ssd_layer_workspace_bytes",
     "ssd_layer_forward",
@@ -73,6 +74,8 @@ _SIGNATURES = {
                               _vp, _vp, _int, _vp, _i64p, _vp, _epi_p, _vp]),
     "ssd_forward": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                            _vp, _vp, _i64p, _vp, _vp, ctypes.c_size_t, _int, _vp]),
+    "ssd_decode_step": (_int, [_dims_p, _int, _vp, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _i64p,
+                                _vp, _i64p, _epi_p, _vp]),
     "ssd_layer_prep": (_int, [_dims_p, _int, _prm_p, _vp, _i64p, _vp, _i64p, _vp, _vp, _vp, _vp, _vp]),
     "ssd_layer_workspace_bytes": (ctypes.c_size_t, [_dims_p, _int]),
     "ssd_layer_forward": (_int, [_dims_p, _int, _prm_p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,

@@ -584,6 +584,66 @@ int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_str
                   y_strides, final_states, ws, w, state_dtype, nullptr, (hipStream_t)stream);
 }
 
+int ssd_decode_step(const ssd_dims* d, int dtype, float* state, const void* x, const int64_t x_strides[2],
+                    const void* bmat, const int64_t b_strides[2], const void* cmat, const int64_t c_strides[2],
+                    const float* a, const float* dt, const int64_t ad_strides[2], void* y,
+                    const int64_t y_strides[2], const ssd_epilogue* epilogue, void* stream) {
+  if (!d) return SSD_ERR_NULL_POINTER;
+  ssd_dims one = *d;  // the sequence dimensions do not apply to one token
+  one.seqlen = one.chunk = 64;
+  int rc = check_dims_impl(&one, dtype);
+  if (rc) return rc;
+  if (d->batch * d->nheads > INT_MAX) return SSD_ERR_TOO_LARGE;
+  if (!state || !x || !x_strides || !bmat || !b_strides || !cmat || !c_strides || !a || !ad_strides || !y ||
+      !y_strides)
+    return SSD_ERR_NULL_POINTER;
+  for (const int64_t* st : {x_strides, b_strides, c_strides, ad_strides, y_strides})
+    if (st[0] < 0 || st[1] < 0) return SSD_ERR_BAD_STRIDE;
+  if (!aligned16(state)) return SSD_ERR_MISALIGNED;
+  const uintptr_t es = elem_size(dtype);
+  for (const void* q : {x, bmat, cmat, static_cast<const void*>(y)})
+    if (reinterpret_cast<uintptr_t>(q) % es != 0) return SSD_ERR_MISALIGNED;
+  if ((reinterpret_cast<uintptr_t>(a) & 3u) != 0 || (dt && (reinterpret_cast<uintptr_t>(dt) & 3u) != 0))
+    return SSD_ERR_MISALIGNED;
+  if (epilogue) {
+    if (epilogue->D && (reinterpret_cast<uintptr_t>(epilogue->D) & 3u) != 0) return SSD_ERR_MISALIGNED;
+    if (epilogue->z) {
+      if (epilogue->z_strides[0] < 0 || epilogue->z_strides[2] < 0 || epilogue->z_strides[3] != 1)
+        return SSD_ERR_BAD_STRIDE;
+      if (reinterpret_cast<uintptr_t>(epilogue->z) % es != 0) return SSD_ERR_MISALIGNED;
+    }
+  }
+  ssd::DecodeArgs p;
+  p.state = state;
+  p.x = x;
+  p.sxb = x_strides[0];
+  p.sxh = x_strides[1];
+  p.bm = bmat;
+  p.sbb = b_strides[0];
+  p.sbg = b_strides[1];
+  p.cm = cmat;
+  p.scb = c_strides[0];
+  p.scg = c_strides[1];
+  p.a = a;
+  p.dt = dt;
+  p.sab = ad_strides[0];
+  p.sah = ad_strides[1];
+  p.y = y;
+  p.syb = y_strides[0];
+  p.syh = y_strides[1];
+  if (epilogue) {
+    p.dskip = epilogue->D;
+    p.z = epilogue->z;
+    p.szb = epilogue->z_strides[0];
+    p.szh = epilogue->z_strides[2];
+  }
+  p.batch = (int)d->batch;
+  p.nheads = (int)d->nheads;
+  p.ngroups = (int)d->ngroups;
+  p.dstate = (int)d->dstate;
+  return hip_status(ssd::launch_decode_step(p, dtype, (hipStream_t)stream));
+}
+
 int ssd_layer_prep(const ssd_dims* d, int dtype, const ssd_layer_params* prm, const void* x_in,
                    const int64_t x_strides[3], const void* dt_in, const int64_t dt_strides[3], void* x_out,
                    float* dt_out, float* a_cumsum, float* chunk_decay, void* stream) {

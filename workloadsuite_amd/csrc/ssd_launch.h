@@ -85,6 +85,27 @@ struct ChunkScanArgs {
   int64_t szb = 0, szl = 0, szh = 0;
 };
 
+// Decode: one token of the recurrence on a [b, h, P, N] f32 state (ssd_decode.hip).
+struct DecodeArgs {
+  float* state;           // [b, h, P, N] contiguous, in place
+  const void* x;          // [b, h, P]
+  int64_t sxb, sxh;
+  const void* bm;         // [b, g, N]
+  int64_t sbb, sbg;
+  const void* cm;
+  int64_t scb, scg;
+  const float* a;         // [b, h] log-decay A dt
+  const float* dt;        // [b, h] or null (1); same strides as a
+  int64_t sab, sah;
+  void* y;                // [b, h, P]
+  int64_t syb, syh;
+  const float* dskip = nullptr;  // [h] or null
+  const void* z = nullptr;       // [b, h, P] or null
+  int64_t szb = 0, szh = 0;
+  int batch, nheads, ngroups, dstate;
+};
+hipError_t launch_decode_step(const DecodeArgs& a, int dtype, hipStream_t stream);
+
 // K0 -- per-(b, c, group) operands of the chunk-256 persistent kernels
 // (ssd_chunk_prep.hip): CB^T blocks for chunk_scan, B^T fragments for chunk_state.
 struct ChunkPrepArgs {

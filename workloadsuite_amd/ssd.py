@@ -42,6 +42,7 @@ __all__ = [
     "state_passing",
     "state_passing_",
     "chunk_scan",
+    "decode_step",
     "layer_prep",
     "ssd_layer",
     "workspace_bytes",
@@ -347,6 +348,55 @@ def chunk_scan(X, B, C, Acs, states, dt=None, prep=None, split=False, D=None, z=
         _ptr(Acs), _ptr(S), _SPLIT_STATES[X.dtype] if split else _STATE_DTYPES[S.dtype], _ptr(Y),
         _lib.strides(Y), _ptr(prep), ctypes.byref(epi) if epi is not None else None, _stream(dev)))
     return Y
+
+
+def decode_step(state, x, B, C, a, dt=None, D=None, z=None):
+    """One token of the recurrence, in place on ``state`` [b, h, P, N] f32
+    (e.g. ssd_forward's final state): state = exp(a) state + dt x B^T, then
+    y = state C (+ D x, * silu(z)).  x, z [b, h, P]; B, C [b, g, N] of x's
+    dtype; a, dt [b, h] f32 (dt None means 1).  Returns y [b, h, P]."""
+    if state.dim() != 4 or state.dtype != torch.float32:
+        raise ValueError("state must be [b, h, P, N] float32")
+    b, h, P, N = state.shape
+    if x.shape != (b, h, P) or B.dim() != 3 or B.shape[0] != b or B.shape[2] != N or C.shape != B.shape:
+        raise ValueError(f"x must be {(b, h, P)} and B, C [b, g, {N}]")
+    g = B.shape[1]
+    if h % g != 0:
+        raise ValueError("n_heads must be divisible by n_groups")
+    if a.shape != (b, h) or (dt is not None and dt.shape != (b, h)):
+        raise ValueError(f"a and dt must be {(b, h)}")
+    if x.dtype not in _DTYPES or B.dtype != x.dtype or C.dtype != x.dtype:
+        raise ValueError("x, B and C must share a supported dtype")
+    if not state.is_contiguous() or state.data_ptr() % 16:
+        raise ValueError("state must be contiguous and 16-byte aligned (it is updated in place)")
+    dev = _device_check(state, x, B, C, a, dt)
+    d = _lib.dims(b, 1, h, P, N, g, 1)
+    x, Bm, Cm = _rows3(x), _rows3(B), _rows3(C)
+    a = _f32_contig(a)
+    dt = _f32_contig(dt)
+    y = torch.empty((b, h, P), dtype=x.dtype, device=dev)
+    epi, _keep = None, ()
+    if D is not None or z is not None:
+        epi = _lib.SSDEpilogue()
+        keep = []
+        if D is not None:
+            D = _f32_contig(D.reshape(h))
+            epi.D = D.data_ptr()
+            keep.append(D)
+        if z is not None:
+            if z.shape != (b, h, P) or z.dtype != x.dtype or z.device != dev:
+                raise ValueError(f"z must match x: {(b, h, P)} {x.dtype}")
+            z = _rows3(z)
+            epi.z = z.data_ptr()
+            epi.z_strides[0], epi.z_strides[1], epi.z_strides[2], epi.z_strides[3] = z.stride(0), 0, z.stride(1), 1
+            keep.append(z)
+        _keep = keep
+    st2 = lambda t: (ctypes.c_int64 * 2)(t.stride(0), t.stride(1))  # noqa: E731
+    _lib.check(_lib.load().ssd_decode_step(
+        ctypes.byref(d), _DTYPES[x.dtype], _ptr(state), _ptr(x), st2(x), _ptr(Bm), st2(Bm), _ptr(Cm), st2(Cm),
+        _ptr(a), _ptr(dt), st2(a), _ptr(y), st2(y), ctypes.byref(epi) if epi is not None else None, _stream(dev)))
+    del _keep
+    return y
 
 
 # ---------------------------------------------------------------------------
