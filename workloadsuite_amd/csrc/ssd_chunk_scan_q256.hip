@@ -32,16 +32,14 @@
 // Data movement.  The next item's x, S_in, Acs and dt are copied global ->
 // LDS by global_load_lds (no VGPRs held) into the second of two LDS buffers
 // while the current item computes; one wait + barrier per item publishes
-// them.  x rows are XOR-swizzled by 16-byte piece at copy time (the copy
-// picks each lane's global address) and S_in rows are copied one per
-// instruction with 16 bytes of padding between rows, so the transposing reads
-// of x and the row reads of S_in are free of bank conflicts.  Every operand
-// read uses a per-lane base computed once plus a compile-time offset.  y
-// stores of an item are issued at the start of the next one so their latency
-// overlaps its compute.
+// them.  x rows and S_in rows are XOR-swizzled by 16-byte piece at copy time
+// (the copy picks each lane's global address), so the transposing reads of x
+// and the row reads of S_in are free of bank conflicts.  Every operand read
+// uses a per-lane base computed once plus a compile-time offset.  y is stored
+// at the end of each item, 16 bytes per lane.
 //
 // Traffic per item: x 32 KB + S_in 32 KB (f32) + Acs 1 KB read, y 32 KB
-// written; B and C per group from L2.  HBM bound at this shape.
+// written; B and C per group from L2.
 //
 // Layer epilogue (EPI, with dt and chunk_prep's operands): y = (y + D[h] x)
 // * silu(z) (MR:116-118) before y's one rounding.  D x reads x from the
