@@ -266,13 +266,30 @@ void set_epilogue(ChunkScanArgs& p, const ssd_epilogue* e) {
   }
 }
 
-// K0 (when it applies), K2, K3, K4 of one forward, after K1 has written acs
-// and decay.  Operands are validated by the caller.
-int run_core(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4], const void* bmat,
-             const int64_t b_strides[4], const void* cmat, const int64_t c_strides[4], const float* dt,
-             const int64_t dt_strides[3], const float* initial_states, void* y, const int64_t y_strides[4],
-             float* final_states, char* ws, const WsLayout& w, int state_dtype, const ssd_epilogue* epi,
-             hipStream_t s) {
+CumsumArgs make_cumsum_args(const ssd_dims* d, const float* a, const int64_t a_strides[3], float* acs,
+                            float* decay) {
+  CumsumArgs p;
+  p.a = a;
+  p.sab = a_strides[0];
+  p.sal = a_strides[1];
+  p.sah = a_strides[2];
+  p.acs = acs;
+  p.decay = decay;
+  p.batch = (int)d->batch;
+  p.nchunks = (int)(d->seqlen / d->chunk);
+  p.nheads = (int)d->nheads;
+  p.chunk = (int)d->chunk;
+  return p;
+}
+
+// K1 (when k1 is given; together with K0 in one launch where K0 applies), K0,
+// K2, K3, K4 of one forward.  Without k1, K1's outputs are already in the
+// workspace.  Operands are validated by the caller.
+int run_core(const ssd_dims* d, int dtype, const CumsumArgs* k1, const void* x, const int64_t x_strides[4],
+             const void* bmat, const int64_t b_strides[4], const void* cmat, const int64_t c_strides[4],
+             const float* dt, const int64_t dt_strides[3], const float* initial_states, void* y,
+             const int64_t y_strides[4], float* final_states, char* ws, const WsLayout& w, int state_dtype,
+             const ssd_epilogue* epi, hipStream_t s) {
   int rc;
   float* acs = reinterpret_cast<float*>(ws + w.acs);
   float* decay = reinterpret_cast<float*>(ws + w.decay);
@@ -284,10 +301,13 @@ int run_core(const ssd_dims* d, int dtype, const void* x, const int64_t x_stride
   // K0: the persistent kernels' per-group operands, once per (b, c, group)
   if (prep_applies(d, dtype)) {
     void* prep = ws + w.prep;
-    if ((rc = hip_status(ssd::launch_chunk_prep(make_prep_args(d, bmat, b_strides, cmat, c_strides, prep), dtype, s))))
+    const ChunkPrepArgs pa = make_prep_args(d, bmat, b_strides, cmat, c_strides, prep);
+    if ((rc = hip_status(k1 ? ssd::launch_chunk_prologue(pa, *k1, dtype, s) : ssd::launch_chunk_prep(pa, dtype, s))))
       return rc;
     sa.btf = prep_btf(d, prep);
     ca.cbf = prep_cbf(prep);
+  } else if (k1) {
+    if ((rc = hip_status(ssd::launch_chunk_cumsum(*k1, s)))) return rc;
   }
   if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, state_dtype, s)))) return rc;
   // f32 states for the chunk-256 chunk_scan: K3 writes them as its hi/lo operand pairs
@@ -456,18 +476,8 @@ int ssd_chunk_cumsum(const ssd_dims* d, const float* a, const int64_t a_strides[
   if (rc) return rc;
   if ((rc = check_scalar_operand(a, a_strides, 3))) return rc;
   if (!a_cumsum || !chunk_decay) return SSD_ERR_NULL_POINTER;
-  CumsumArgs p;
-  p.a = a;
-  p.sab = a_strides[0];
-  p.sal = a_strides[1];
-  p.sah = a_strides[2];
-  p.acs = a_cumsum;
-  p.decay = chunk_decay;
-  p.batch = (int)d->batch;
-  p.nchunks = (int)(d->seqlen / d->chunk);
-  p.nheads = (int)d->nheads;
-  p.chunk = (int)d->chunk;
-  return hip_status(ssd::launch_chunk_cumsum(p, (hipStream_t)stream));
+  return hip_status(ssd::launch_chunk_cumsum(make_cumsum_args(d, a, a_strides, a_cumsum, chunk_decay),
+                                            (hipStream_t)stream));
 }
 
 size_t ssd_chunk_prep_bytes(const ssd_dims* d) {
@@ -577,10 +587,9 @@ int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_str
     return SSD_ERR_MISALIGNED;
 
   char* ws = static_cast<char*>(workspace);
-  float* acs = reinterpret_cast<float*>(ws + w.acs);
-  float* decay = reinterpret_cast<float*>(ws + w.decay);
-  if ((rc = ssd_chunk_cumsum(d, a, a_strides, acs, decay, stream))) return rc;
-  return run_core(d, dtype, x, x_strides, bmat, b_strides, cmat, c_strides, dt, dt_strides, initial_states, y,
+  const CumsumArgs k1 = make_cumsum_args(d, a, a_strides, reinterpret_cast<float*>(ws + w.acs),
+                                         reinterpret_cast<float*>(ws + w.decay));
+  return run_core(d, dtype, &k1, x, x_strides, bmat, b_strides, cmat, c_strides, dt, dt_strides, initial_states, y,
                   y_strides, final_states, ws, w, state_dtype, nullptr, (hipStream_t)stream);
 }
 
@@ -715,8 +724,8 @@ int ssd_layer_forward(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
   epi.z_strides[1] = z_strides[1];
   epi.z_strides[2] = P * z_strides[2];
   epi.z_strides[3] = z_strides[2];
-  return run_core(d, dtype, x_out, xs4, bmat, b_strides, cmat, c_strides, dt_out, dts, nullptr, y, ys4, nullptr, core,
-                  w.cw, SSD_DTYPE_F32, &epi, s);
+  return run_core(d, dtype, nullptr, x_out, xs4, bmat, b_strides, cmat, c_strides, dt_out, dts, nullptr, y, ys4,
+                  nullptr, core, w.cw, SSD_DTYPE_F32, &epi, s);
 }
 
 }  // extern "C"

@@ -14,8 +14,15 @@
 // XOR-swizzled by 16-byte piece so the 16 rows of an operand read hit
 // distinct banks), then each wave forms its CB^T blocks with the same MFMA
 // sequence as chunk_scan's own fallback, so both give bit-identical values.
+//
+// The forward launches K0 and K1 (ssd_cumsum_body.h) together: the first
+// workgroups of the grid do K0, the rest two K1 blocks each (one per 256
+// threads) on the same LDS.  Both are short and independent; together they
+// fill the GPU that K0's few workgroups alone leave mostly idle, and one
+// kernel boundary goes away.
 #include <cstdint>
 
+#include "ssd_cumsum_body.h"
 #include "ssd_device.h"
 #include "ssd_launch.h"
 #include "../../include/ssd.h"
@@ -29,19 +36,21 @@ constexpr int kNW = 8;
 constexpr int kThreads = 64 * kNW;
 constexpr int kNPair = kQ / 32 + 1;  // CB^T steps per wave (two row tiles)
 
+template <int NK> constexpr int prep_lds_bytes() { return 2 * kQ * (64 * NK); }  // B and C rows
+
+// K0 for group bcg = (b * nchunks + c) * ngroups + grp, on lds (prep_lds_bytes, 1 KB aligned).
 template <typename T, int NK>
-__global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkPrepArgs p) {
+__device__ __forceinline__ void prep_body(const ChunkPrepArgs& p, int bcg, unsigned char* lds) {
   constexpr int N = 32 * NK;
   constexpr int RB = N * 2;      // bytes per B / C row
   constexpr int PPR = RB / 16;   // 16-byte pieces per row
   constexpr int RPD = 1024 / RB; // rows per 64-lane copy
   constexpr int NTILE = N / 16;
-  __shared__ __attribute__((aligned(1024))) unsigned char bl[kQ * RB];
-  __shared__ __attribute__((aligned(1024))) unsigned char cl[kQ * RB];
+  unsigned char* bl = lds;
+  unsigned char* cl = lds + kQ * RB;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, i = lane & 15;
-  const int bcg = blockIdx.x;  // (b * nchunks + c) * ngroups + grp
   const int grp = bcg % p.ngroups, bc = bcg / p.ngroups;
   const int c = bc % p.nchunks, b = bc / p.nchunks;
   auto sw = [](int r) __attribute__((always_inline)) { return PPR >= 16 ? (r & 15) : ((r >> 1) & 7); };
@@ -104,12 +113,48 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkPrepArgs p) {
   }
 }
 
+template <typename T, int NK>
+__global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkPrepArgs p) {
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[prep_lds_bytes<NK>()];
+  prep_body<T, NK>(p, blockIdx.x, lds);
+}
+
+// K0 for the first nprep workgroups, then two K1 blocks (chunk 256) per workgroup.
+template <typename T, int NK>
+__global__ __launch_bounds__(kThreads) void chunk_prologue_kernel(ChunkPrepArgs p, CumsumArgs ca, int nprep) {
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[prep_lds_bytes<NK>()];
+  static_assert(2 * sizeof(CumsumTile<kQ>) <= prep_lds_bytes<NK>(), "K1 tiles fit in K0's LDS");
+  if ((int)blockIdx.x < nprep) {
+    prep_body<T, NK>(p, blockIdx.x, lds);
+    return;
+  }
+  const int half = threadIdx.x >> 8, t = threadIdx.x & 255;
+  const int blk = 2 * ((int)blockIdx.x - nprep) + half;
+  CumsumTile<kQ>& tile = *reinterpret_cast<CumsumTile<kQ>*>(lds + half * sizeof(CumsumTile<kQ>));
+  const bool valid = blk < cumsum_blocks(ca);
+  if (valid) cumsum_load<kQ, float, false>(ca, blk, t, tile);
+  __syncthreads();
+  if (valid) cumsum_scan<kQ>(ca, blk, t / kWave, t % kWave, tile);
+}
+
 template <typename T>
 hipError_t launch_t(const ChunkPrepArgs& a, hipStream_t stream) {
   const unsigned grid = (unsigned)(a.batch * a.nchunks * a.ngroups);
   switch (a.dstate) {
     case 64: chunk_prep_kernel<T, 2><<<grid, kThreads, 0, stream>>>(a); break;
     case 128: chunk_prep_kernel<T, 4><<<grid, kThreads, 0, stream>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_prologue_t(const ChunkPrepArgs& a, const CumsumArgs& ca, hipStream_t stream) {
+  const int nprep = a.batch * a.nchunks * a.ngroups;
+  const unsigned grid = (unsigned)(nprep + (cumsum_blocks(ca) + 1) / 2);
+  switch (a.dstate) {
+    case 64: chunk_prologue_kernel<T, 2><<<grid, kThreads, 0, stream>>>(a, ca, nprep); break;
+    case 128: chunk_prologue_kernel<T, 4><<<grid, kThreads, 0, stream>>>(a, ca, nprep); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -124,6 +169,13 @@ hipError_t launch_chunk_prep(const ChunkPrepArgs& a, int dtype, hipStream_t stre
   if (a.chunk != kQ) return hipErrorInvalidValue;
   if (dtype == SSD_DTYPE_BF16) return launch_t<bf16>(a, stream);
   if (dtype == SSD_DTYPE_F16) return launch_t<f16>(a, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_chunk_prologue(const ChunkPrepArgs& a, const CumsumArgs& ca, int dtype, hipStream_t stream) {
+  if (a.chunk != kQ || ca.chunk != kQ || ca.dt_raw) return hipErrorInvalidValue;
+  if (dtype == SSD_DTYPE_BF16) return launch_prologue_t<bf16>(a, ca, stream);
+  if (dtype == SSD_DTYPE_F16) return launch_prologue_t<f16>(a, ca, stream);
   return hipErrorInvalidValue;
 }
 

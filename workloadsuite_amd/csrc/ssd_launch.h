@@ -120,6 +120,9 @@ struct ChunkPrepArgs {
 size_t chunk_prep_cb_bytes(int64_t groups);
 size_t chunk_prep_bt_bytes(int64_t groups, int dstate);
 hipError_t launch_chunk_prep(const ChunkPrepArgs& a, int dtype, hipStream_t stream);
+// K0 and K1 (chunk 256, from A) in one launch: bit-identical to launching
+// launch_chunk_prep and launch_chunk_cumsum one after the other.
+hipError_t launch_chunk_prologue(const ChunkPrepArgs& a, const CumsumArgs& ca, int dtype, hipStream_t stream);
 
 // Compute units of the current device (cached per device id after the first
 // query; 0 when the query fails).
