@@ -179,3 +179,25 @@ def test_chunk_scan_epilogue_rejects_mismatched_gate():
     st = torch.zeros(1, 1, 2, 64, 16, device=DEV)
     with pytest.raises(ValueError, match="z must match"):
         S.chunk_scan(X, B, B, Acs, st, z=torch.zeros(1, 64, 2, 32, device=DEV))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("N,g", [(128, 2), (64, 4)])
+def test_ssd_layer_equals_its_kernels_one_by_one(dtype, N, g):
+    """ssd_layer (conv, then K1's layer variant inside K0's launch, K0 writing
+    CB^T in the input type for K4's epilogue variant) against the public
+    entry points called one by one: bit-identical."""
+    say("ssd_layer == kernels", dtype, N, g)
+    h, P, Q, L, b = 8, 64, 256, 512, 2
+    proj, prm = layer_case(dtype, b=b, L=L, h=h, P=P, g=g, N=N)
+    pd = proj.to(DEV)
+    x, z, B, C, dt = split(pd, h, P, g, N)
+    dev = {k: v.to(DEV) for k, v in prm.items()}
+    y = S.ssd_layer(x, z, B, C, dt, dev["conv_w"], dev["conv_b"], dev["dt_bias"], dev["A_log"], dev["D"], 64, h)
+    X, dto, Acs, dec = S.layer_prep(x, dt, dev["conv_w"], dev["conv_b"], dev["dt_bias"], dev["A_log"], Q, h)
+    prep = S.chunk_prep(B, C, Q)
+    st = S.chunk_state(X, B, Acs, dt=dto, prep=prep)
+    S_in, _ = S.state_passing(st, dec, split=dtype)
+    yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dto, prep=prep, split=True, D=dev["D"], z=z.reshape(b, L, h, P))
+    torch.cuda.synchronize()
+    assert torch.equal(y, yk.reshape(b, L, h * P))

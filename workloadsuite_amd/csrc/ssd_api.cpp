@@ -301,7 +301,11 @@ int run_core(const ssd_dims* d, int dtype, const CumsumArgs* k1, const void* x, 
   // K0: the persistent kernels' per-group operands, once per (b, c, group)
   if (prep_applies(d, dtype)) {
     void* prep = ws + w.prep;
-    const ChunkPrepArgs pa = make_prep_args(d, bmat, b_strides, cmat, c_strides, prep);
+    ChunkPrepArgs pa = make_prep_args(d, bmat, b_strides, cmat, c_strides, prep);
+    // the epilogue variant of K4 keeps CB^T in the input type: K0 writes it so
+    ca.cbf = prep_cbf(prep);
+    pa.cb16 = epi && ssd::chunk_scan_persistent_supported(ca, dtype);
+    ca.cb16 = pa.cb16;
     if ((rc = hip_status(k1 ? ssd::launch_chunk_prologue(pa, *k1, dtype, s) : ssd::launch_chunk_prep(pa, dtype, s))))
       return rc;
     sa.btf = prep_btf(d, prep);
@@ -379,22 +383,9 @@ int check_layer_grid(const ssd_dims* d) {
   return SSD_OK;
 }
 
-int launch_layer_prep(const ssd_dims* d, int dtype, const ssd_layer_params* prm, const void* x_in,
-                      const int64_t x_strides[3], const void* dt_in, const int64_t dt_strides[3], void* x_out,
-                      float* dt_out, float* acs, float* decay, hipStream_t s) {
-  ConvArgs cv;
-  cv.x = x_in;
-  cv.sxb = x_strides[0];
-  cv.sxl = x_strides[1];
-  cv.w = prm->conv_w;
-  cv.bias = prm->conv_b;
-  cv.y = x_out;
-  cv.batch = (int)d->batch;
-  cv.seqlen = (int)d->seqlen;
-  cv.channels = (int)(d->nheads * d->headdim);
-  cv.kwidth = (int)prm->conv_kernel;
-  int rc;
-  if ((rc = hip_status(ssd::launch_conv_silu(cv, dtype, s)))) return rc;
+// K1's layer variant: dt = softplus(dt_raw + dt_bias), A_dt = -exp(A_log) dt, then the cumsum.
+CumsumArgs make_raw_cumsum_args(const ssd_dims* d, int dtype, const ssd_layer_params* prm, const void* dt_in,
+                                const int64_t dt_strides[3], float* dt_out, float* acs, float* decay) {
   CumsumArgs ca;
   ca.a = nullptr;
   ca.sab = ca.sal = ca.sah = 0;
@@ -412,7 +403,32 @@ int launch_layer_prep(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
   ca.a_log = prm->A_log;
   ca.dt_out = dt_out;
   ca.raw_dtype = dtype;
-  return hip_status(ssd::launch_chunk_cumsum(ca, s));
+  return ca;
+}
+
+int launch_conv(const ssd_dims* d, int dtype, const ssd_layer_params* prm, const void* x_in,
+                const int64_t x_strides[3], void* x_out, hipStream_t s) {
+  ConvArgs cv;
+  cv.x = x_in;
+  cv.sxb = x_strides[0];
+  cv.sxl = x_strides[1];
+  cv.w = prm->conv_w;
+  cv.bias = prm->conv_b;
+  cv.y = x_out;
+  cv.batch = (int)d->batch;
+  cv.seqlen = (int)d->seqlen;
+  cv.channels = (int)(d->nheads * d->headdim);
+  cv.kwidth = (int)prm->conv_kernel;
+  return hip_status(ssd::launch_conv_silu(cv, dtype, s));
+}
+
+int launch_layer_prep(const ssd_dims* d, int dtype, const ssd_layer_params* prm, const void* x_in,
+                      const int64_t x_strides[3], const void* dt_in, const int64_t dt_strides[3], void* x_out,
+                      float* dt_out, float* acs, float* decay, hipStream_t s) {
+  int rc;
+  if ((rc = launch_conv(d, dtype, prm, x_in, x_strides, x_out, s))) return rc;
+  return hip_status(
+      ssd::launch_chunk_cumsum(make_raw_cumsum_args(d, dtype, prm, dt_in, dt_strides, dt_out, acs, decay), s));
 }
 
 }  // namespace
@@ -710,10 +726,11 @@ int ssd_layer_forward(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
   const hipStream_t s = (hipStream_t)stream;
   const ssd_dims e = layer_core_dims(d, dtype);
   d = &e;
-  if ((rc = launch_layer_prep(d, dtype, prm, x_in, x_strides, dt_in, dt_strides, x_out, dt_out,
-                              reinterpret_cast<float*>(core + w.cw.acs), reinterpret_cast<float*>(core + w.cw.decay),
-                              s)))
-    return rc;
+  // conv, then K1's layer variant inside the core's first launch (with K0 where it applies)
+  if ((rc = launch_conv(d, dtype, prm, x_in, x_strides, x_out, s))) return rc;
+  const CumsumArgs k1 = make_raw_cumsum_args(d, dtype, prm, dt_in, dt_strides, dt_out,
+                                             reinterpret_cast<float*>(core + w.cw.acs),
+                                             reinterpret_cast<float*>(core + w.cw.decay));
   const int64_t h = d->nheads, L = d->seqlen;
   const int64_t xs4[4] = {L * h * P, h * P, P, 1};
   const int64_t dts[3] = {L * h, h, 1};
@@ -724,7 +741,7 @@ int ssd_layer_forward(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
   epi.z_strides[1] = z_strides[1];
   epi.z_strides[2] = P * z_strides[2];
   epi.z_strides[3] = z_strides[2];
-  return run_core(d, dtype, nullptr, x_out, xs4, bmat, b_strides, cmat, c_strides, dt_out, dts, nullptr, y, ys4,
+  return run_core(d, dtype, &k1, x_out, xs4, bmat, b_strides, cmat, c_strides, dt_out, dts, nullptr, y, ys4,
                   nullptr, core, w.cw, SSD_DTYPE_F32, &epi, s);
 }
 

@@ -7,6 +7,9 @@
 //        D-fragment order chunk_scan keeps in registers: wave w, step k
 //        (row tile w's s block k for k < w/2 + 1, else row tile 15-w's s block
 //        8-k), sub-tile st, lane.  Sub-tiles above the diagonal are 0.
+//        With cb16 the same values are written rounded to T, [step][lane]
+//        16 bytes (both sub-tiles), for chunk_scan's epilogue variant, which
+//        holds CB^T in T.
 //   btf  the B^T MFMA operands of chunk_state (MR:148 contracts over the
 //        chunk's tokens): n tile nt, 32-token step ks, lane (g, i) holds
 //        B[32 ks + slot_token(g, j)][16 nt + i] for j = 0..7.
@@ -95,7 +98,13 @@ __device__ __forceinline__ void prep_body(const ChunkPrepArgs& p, int bcg, unsig
       const bool live = 2 * sb + st <= t;
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj) d[jj] = live ? d[jj] : 0.f;
-      out[(k * 2 + st) * 64] = d;
+      if (p.cb16) {
+        // [k][lane] 16 bytes: sub-tile 0's 4 values, then sub-tile 1's, in T
+        vec4<T>* o16 = reinterpret_cast<vec4<T>*>(p.cbf) + ((int64_t)(bcg * kNW + wave) * kNPair * 64 + lane) * 2;
+        o16[k * 64 * 2 + st] = __builtin_convertvector(d, vec4<T>);
+      } else {
+        out[(k * 2 + st) * 64] = d;
+      }
     }
   }
 
@@ -120,7 +129,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkPrepArgs p) {
 }
 
 // K0 for the first nprep workgroups, then two K1 blocks (chunk 256) per workgroup.
-template <typename T, int NK>
+template <typename T, int NK, typename R, bool RAW>
 __global__ __launch_bounds__(kThreads) void chunk_prologue_kernel(ChunkPrepArgs p, CumsumArgs ca, int nprep) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds[prep_lds_bytes<NK>()];
   static_assert(2 * sizeof(CumsumTile<kQ>) <= prep_lds_bytes<NK>(), "K1 tiles fit in K0's LDS");
@@ -132,7 +141,7 @@ __global__ __launch_bounds__(kThreads) void chunk_prologue_kernel(ChunkPrepArgs 
   const int blk = 2 * ((int)blockIdx.x - nprep) + half;
   CumsumTile<kQ>& tile = *reinterpret_cast<CumsumTile<kQ>*>(lds + half * sizeof(CumsumTile<kQ>));
   const bool valid = blk < cumsum_blocks(ca);
-  if (valid) cumsum_load<kQ, float, false>(ca, blk, t, tile);
+  if (valid) cumsum_load<kQ, R, RAW>(ca, blk, t, tile);
   __syncthreads();
   if (valid) cumsum_scan<kQ>(ca, blk, t / kWave, t % kWave, tile);
 }
@@ -148,13 +157,13 @@ hipError_t launch_t(const ChunkPrepArgs& a, hipStream_t stream) {
   return hipGetLastError();
 }
 
-template <typename T>
+template <typename T, typename R, bool RAW>
 hipError_t launch_prologue_t(const ChunkPrepArgs& a, const CumsumArgs& ca, hipStream_t stream) {
   const int nprep = a.batch * a.nchunks * a.ngroups;
   const unsigned grid = (unsigned)(nprep + (cumsum_blocks(ca) + 1) / 2);
   switch (a.dstate) {
-    case 64: chunk_prologue_kernel<T, 2><<<grid, kThreads, 0, stream>>>(a, ca, nprep); break;
-    case 128: chunk_prologue_kernel<T, 4><<<grid, kThreads, 0, stream>>>(a, ca, nprep); break;
+    case 64: chunk_prologue_kernel<T, 2, R, RAW><<<grid, kThreads, 0, stream>>>(a, ca, nprep); break;
+    case 128: chunk_prologue_kernel<T, 4, R, RAW><<<grid, kThreads, 0, stream>>>(a, ca, nprep); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -173,9 +182,13 @@ hipError_t launch_chunk_prep(const ChunkPrepArgs& a, int dtype, hipStream_t stre
 }
 
 hipError_t launch_chunk_prologue(const ChunkPrepArgs& a, const CumsumArgs& ca, int dtype, hipStream_t stream) {
-  if (a.chunk != kQ || ca.chunk != kQ || ca.dt_raw) return hipErrorInvalidValue;
-  if (dtype == SSD_DTYPE_BF16) return launch_prologue_t<bf16>(a, ca, stream);
-  if (dtype == SSD_DTYPE_F16) return launch_prologue_t<f16>(a, ca, stream);
+  if (a.chunk != kQ || ca.chunk != kQ) return hipErrorInvalidValue;
+  // the layer variant's raw dt has the inputs' type
+  if (ca.dt_raw && ca.raw_dtype != dtype) return hipErrorInvalidValue;
+  if (dtype == SSD_DTYPE_BF16)
+    return ca.dt_raw ? launch_prologue_t<bf16, bf16, true>(a, ca, stream) : launch_prologue_t<bf16, float, false>(a, ca, stream);
+  if (dtype == SSD_DTYPE_F16)
+    return ca.dt_raw ? launch_prologue_t<f16, f16, true>(a, ca, stream) : launch_prologue_t<f16, float, false>(a, ca, stream);
   return hipErrorInvalidValue;
 }
 

@@ -77,6 +77,7 @@ struct ScanArgs32 {
   const void* states;
   void* y;
   const float* cbf;  // chunk_prep's CB^T fragments, or null
+  int cb16;          // ... rounded to T (the epilogue variant)
   int presplit;      // f32 S_in already stored as [hi x8 | lo x8] pairs
   const float* dskip;  // epilogue: skip weights [h], or null
   const void* z;       // epilogue: gate [b, L, h, P], or null
@@ -297,8 +298,21 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     }
     if constexpr (PREP) {
       // precomputed by chunk_prep in this order: one round of independent loads
-      const f32x4* cb = reinterpret_cast<const f32x4*>(p.cbf) +
-                        ((((int64_t)r.b * p.nchunks + r.c) * p.ngroups + r.grp) * kNW + wave) * (kNPair * 2 * 64) + lane_o;
+      const int64_t wbase = (((int64_t)r.b * p.nchunks + r.c) * p.ngroups + r.grp) * kNW + wave;
+      if constexpr (EPI) {
+        if (p.cb16) {
+          // rounded to T by chunk_prep already (the same values CbStep would hold)
+          const frag8<T>* cb = reinterpret_cast<const frag8<T>*>(p.cbf) + wbase * (kNPair * 64) + lane_o;
+#pragma unroll
+          for (int k = 0; k < kNPair; ++k) {
+            const frag8<T> v = cb[k * 64];
+            cbc[k].v[0] = v.lo;
+            cbc[k].v[1] = v.hi;
+          }
+          return;
+        }
+      }
+      const f32x4* cb = reinterpret_cast<const f32x4*>(p.cbf) + wbase * (kNPair * 2 * 64) + lane_o;
 #pragma unroll
       for (int k = 0; k < kNPair; ++k)
 #pragma unroll
@@ -613,6 +627,7 @@ ScanArgs32 narrow(const ChunkScanArgs& a) {
   n.states = a.states;
   n.y = a.y;
   n.cbf = a.cbf;
+  n.cb16 = a.cb16 ? 1 : 0;
   n.presplit = a.presplit ? 1 : 0;
   n.dskip = a.dskip;
   n.z = a.z;

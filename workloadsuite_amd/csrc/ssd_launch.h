@@ -78,6 +78,7 @@ struct ChunkScanArgs {
   int64_t syb, syl, syh;  // y [b, L, h, P], unit stride over P
   int batch, nchunks, nheads, ngroups, dstate, chunk;
   const float* cbf = nullptr;  // optional chunk_prep CB^T fragments (persistent kernel)
+  bool cb16 = false;           // ... rounded to the input type (the epilogue variant reads those)
   bool presplit = false;       // f32 states already split by state_passing (split_dtype)
   // optional epilogue: y = (y + dskip[h] x) * silu(z)
   const float* dskip = nullptr;  // [h]
@@ -116,12 +117,15 @@ struct ChunkPrepArgs {
   int batch, nchunks, ngroups, dstate, chunk;
   float* cbf;  // chunk_prep_cb_bytes(batch * nchunks * ngroups)
   void* btf;   // chunk_prep_bt_bytes(batch * nchunks * ngroups, dstate)
+  // CB^T rounded to the input type (half of chunk_prep_cb_bytes), for chunk_scan's epilogue variant
+  bool cb16 = false;
 };
 size_t chunk_prep_cb_bytes(int64_t groups);
 size_t chunk_prep_bt_bytes(int64_t groups, int dstate);
 hipError_t launch_chunk_prep(const ChunkPrepArgs& a, int dtype, hipStream_t stream);
-// K0 and K1 (chunk 256, from A) in one launch: bit-identical to launching
-// launch_chunk_prep and launch_chunk_cumsum one after the other.
+// K0 and K1 (chunk 256; from A, or the layer variant from raw dt) in one
+// launch: bit-identical to launching launch_chunk_prep and
+// launch_chunk_cumsum one after the other.
 hipError_t launch_chunk_prologue(const ChunkPrepArgs& a, const CumsumArgs& ca, int dtype, hipStream_t stream);
 
 // Compute units of the current device (cached per device id after the first
