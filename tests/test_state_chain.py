@@ -1,0 +1,68 @@
+"""The chunk-256 forward runs chunk_state and state_passing as one launch
+(each workgroup walks one (batch, head) chain of chunks with the running
+state in registers, workloads/mamba/model_ref.py:144-157) when the chains
+spread evenly over the CUs -- always when there are at most as many chains as
+CUs, as in every shape here except the last one (640 chains: 3 per CU at
+256 CUs, also fused).  That launch must give exactly what the two kernels
+give one after the other: ssd_forward against the public per-kernel entry
+points, bit for bit (Y and the final state), with and without dt and an
+initial state, both 16-bit types, both dstates, several groups.  The
+per-kernel path itself is held to the oracle by the parity tests."""
+
+import pytest
+import torch
+
+from workloadsuite_amd import ssd as S
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+
+
+def case(dtype, b, L, h, P, N, g, seed):
+    gen = torch.Generator().manual_seed(seed)
+    X = torch.randn(b, L, h, P, generator=gen).to(dtype)
+    A = -torch.rand(b, L, h, generator=gen) * 0.2
+    B = (torch.randn(b, L, g, N, generator=gen) * N ** -0.5).to(dtype)
+    C = (torch.randn(b, L, g, N, generator=gen) * N ** -0.5).to(dtype)
+    dt = torch.rand(b, L, h, generator=gen) + 0.1
+    init = torch.randn(b, h, P, N, generator=gen)
+    return [t.to(DEV) for t in (X, A, B, C, dt, init)]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("N,g,h", [(128, 1, 8), (64, 2, 6), (128, 4, 12)])
+@pytest.mark.parametrize("with_dt,with_init", [(True, True), (False, False), (True, False)])
+def test_forward_equals_kernels_one_by_one(dtype, N, g, h, with_dt, with_init):
+    b, L, P, Q = 2, 1280, 64, 256
+    print("CASE chain", dtype, N, g, h, with_dt, with_init, flush=True)
+    X, A, B, C, dt, init = case(dtype, b, L, h, P, N, g, seed=N + g + h)
+    dt = dt if with_dt else None
+    init = init if with_init else None
+    Y, final = S.ssd_forward(X, A, B, C, Q, dt=dt, initial_states=init, return_final_states=True)
+
+    Acs, decay = S.chunk_cumsum(A, Q)
+    prep = S.chunk_prep(B, C, Q)
+    st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
+    S_in, fk = S.state_passing(st, decay, initial_states=init, split=dtype)
+    Yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dt, prep=prep, split=True)
+    torch.cuda.synchronize()
+    assert torch.equal(final, fk)
+    assert torch.equal(Y, Yk)
+
+
+def test_single_chunk_and_many_chains():
+    """One chunk per chain (the loop body runs once) and more chains than the
+    GPU holds at once."""
+    for (b, L, h) in [(3, 256, 5), (4, 512, 160)]:
+        print("CASE chain shape", b, L, h, flush=True)
+        X, A, B, C, dt, init = case(torch.bfloat16, b, L, h, 64, 128, 1, seed=L + h)
+        Y, final = S.ssd_forward(X, A, B, C, 256, dt=dt, initial_states=init, return_final_states=True)
+        Acs, decay = S.chunk_cumsum(A, 256)
+        prep = S.chunk_prep(B, C, 256)
+        st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
+        S_in, fk = S.state_passing(st, decay, initial_states=init, split=torch.bfloat16)
+        Yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dt, prep=prep, split=True)
+        torch.cuda.synchronize()
+        assert torch.equal(final, fk)
+        assert torch.equal(Y, Yk)

@@ -313,14 +313,19 @@ int run_core(const ssd_dims* d, int dtype, const CumsumArgs* k1, const void* x, 
   } else if (k1) {
     if ((rc = hip_status(ssd::launch_chunk_cumsum(*k1, s)))) return rc;
   }
-  if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, state_dtype, s)))) return rc;
   // f32 states for the chunk-256 chunk_scan: K3 writes them as its hi/lo operand pairs
   StatePassingArgs pa = make_sp_args(d, states, decay, initial_states, final_states);
   if (state_dtype == SSD_DTYPE_F32 && prep_applies(d, dtype) && ssd::chunk_scan_persistent_supported(ca, dtype)) {
     pa.split_dtype = dtype;
     ca.presplit = true;
   }
-  if ((rc = hip_status(ssd::launch_state_passing(pa, state_dtype, s)))) return rc;
+  if (pa.split_dtype && ssd::chunk_state_chain_preferred(sa, dtype)) {
+    // K2 and K3 as one launch: the local states stay in registers (same bits)
+    if ((rc = hip_status(ssd::launch_chunk_state_chain(sa, pa, dtype, s)))) return rc;
+  } else {
+    if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, state_dtype, s)))) return rc;
+    if ((rc = hip_status(ssd::launch_state_passing(pa, state_dtype, s)))) return rc;
+  }
   return hip_status(ssd::launch_chunk_scan(ca, dtype, state_dtype, s));
 }
 

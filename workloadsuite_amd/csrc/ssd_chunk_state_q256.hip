@@ -284,6 +284,189 @@ hipError_t launch_ts(const ChunkStateArgs& a, hipStream_t stream) {
   }
 }
 
+
+// ---- K2 + K3 in one launch: chunk_state with the state recurrence ----
+//
+// One workgroup (8 waves, the wave layout of one half above) per (b, h)
+// chain walks the chunks in order.  Per chunk it computes the chunk's local
+// state exactly as chunk_state_q256_kernel does, then advances the running
+// state held in registers, h <- h * decay[c] + local (workloads/mamba/
+// model_ref.py:152-157), after storing the state entering the chunk, S_in[c],
+// as chunk_scan's hi/lo operand pairs (the layout of state_passing's split
+// kernel).  The per-chunk local states never reach memory: per chunk the
+// chain reads x (32 KB) and writes S_in (32 KB) instead of K2's 32 KB write
+// plus K3's 32 KB read and 32 KB write.  Same arithmetic in the same order
+// as K2 then K3 (f32 local state, one f32 FMA per element and chunk), so the
+// result is bit-identical.
+//
+// Pipelining per chunk step: the next chunk's x, Acs and dt copies are
+// issued in K steps 0-3 (after the S_in stores), and each B^T fragment of
+// the next chunk is loaded into its register as soon as the current chunk's
+// weighting has consumed it, so the per-chunk group operands arrive under
+// the current chunk's compute.
+template <typename T, int NK, bool HAS_DT>
+__global__ __launch_bounds__(64 * kNW) __attribute__((amdgpu_waves_per_eu(4)))
+void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp) {
+  constexpr int N = 32 * NK;
+  constexpr int NTILE = N / 16;
+  constexpr int PTW = NTILE / 2;
+  static_assert(PTW <= kXBlocks / kNW, "S_in stores precede the last copy part");
+  __shared__ __attribute__((aligned(1024))) T xr[2][kQ * kP];
+  __shared__ __attribute__((aligned(16))) float ar[2][kQ];
+  __shared__ __attribute__((aligned(16))) float dr[HAS_DT ? 2 : 1][HAS_DT ? kQ : 4];
+  __shared__ __attribute__((aligned(16))) float wr[kQ];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  __builtin_assume(wave < kNW);
+  const int g = lane >> 4, i = lane & 15;
+  const int bh = blockIdx.x;  // b * nheads + h
+  const int h = bh % p.nheads, b = bh / p.nheads;
+  const int grp = h / (p.nheads / p.ngroups);
+  const int nt = wave % NTILE, pt0 = (wave / NTILE) * PTW;
+  const bool odd = g & 1;
+
+  int xoff[PTW];
+  {
+    const int r = 4 * g + (i >> 2), x7 = r & 7;
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) {
+      const int pt = pt0 + q;
+      xoff[q] = r * kP + 8 * ((2 * pt + ((i & 3) >> 1)) ^ x7) + 4 * (i & 1);
+    }
+  }
+  const int64_t xcopy = (int64_t)(lane >> 3) * p.sxl + 8 * ((lane & 7) ^ (lane >> 3));
+  // this lane's states: row 16 pt + i, columns 16 nt + 4 g .. + 3 of the [P][N] state
+  const int srow = (16 * pt0 + i) * N + 16 * nt + 4 * g;
+  const T* xchain = reinterpret_cast<const T*>(p.x) + b * p.sxb + h * p.sxh + xcopy;
+  const float* achain = p.acs + (int64_t)bh * p.nchunks * kQ;
+  const float* dchain = HAS_DT ? p.dt + b * p.sdb + h * p.sdh : nullptr;
+
+  const uint32_t xr_lds = lds_offset(&xr[0][0]), ar_lds = lds_offset(&ar[0][0]);
+  const uint32_t dr_lds = lds_offset(&dr[0][0]);
+  // part m (0..3) of chunk c's copy into buffer bs
+  auto issue_copy_part = [&](int c, int bs, int m) __attribute__((always_inline)) {
+    const int64_t l0 = (int64_t)c * kQ;
+    const int blk = wave + kNW * m;
+    dma16_at(xchain + (l0 + 8 * blk) * p.sxl, xr_lds + (uint32_t)((bs * kQ * kP + blk * 512) * (int)sizeof(T)));
+    if (m != 0) return;
+    if (wave == kNW - 1) dma16_at(achain + (int64_t)c * kQ + 4 * lane, ar_lds + (uint32_t)(bs * kQ * 4));
+    if constexpr (HAS_DT) {
+      if (wave < kQ / 64) dma4_at(dchain + (l0 + 64 * wave + lane) * p.sdl, dr_lds + (uint32_t)((bs * kQ + 64 * wave) * 4));
+    }
+  };
+  auto tabulate = [&](int bs) __attribute__((always_inline)) {
+    if (tid < kQ) {
+      float w = __builtin_amdgcn_exp2f((ar[bs][kQ - 1] - ar[bs][tid]) * kLog2e);
+      if constexpr (HAS_DT) w *= dr[bs][tid];
+      wr[tid] = w;
+    }
+  };
+  // chunk_prep's B^T fragments of chunk c, this wave's n tile
+  auto btf_of = [&](int c) __attribute__((always_inline)) {
+    return reinterpret_cast<const frag8<T>*>(p.btf) +
+           ((((int64_t)b * p.nchunks + c) * p.ngroups + grp) * NTILE + nt) * (kKS * 64) + lane;
+  };
+
+  // running state: S_in of the current chunk
+  f32x4 st[PTW];
+#pragma unroll
+  for (int q = 0; q < PTW; ++q)
+    st[q] = sp.init ? *reinterpret_cast<const f32x4*>(sp.init + (int64_t)bh * (kP * N) + srow + 16 * N * q)
+                    : f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // S_in of chunk c, as [hi x8 | lo x8] of T per 8 consecutive states: lane
+  // pairs (g, g ^ 1) swap halves so that the even-g lane stores the 8 hi and
+  // the odd-g lane the 8 lo values, each at its own f32 state address.
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  auto store_sin = [&](int c, int q) __attribute__((always_inline)) {
+    vec4<T> hi, lo;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      hi[k] = from_f32<T>(st[q][k]);
+      lo[k] = from_f32<T>(st[q][k] - to_f32<T>(hi[k]));
+    }
+    const u32x2 hw = __builtin_bit_cast(u32x2, hi), lw = __builtin_bit_cast(u32x2, lo);
+    const u32x2 give = odd ? hw : lw, keep = odd ? lw : hw;
+    u32x2 got;
+    got[0] = (uint32_t)__shfl_xor((int)give[0], 16);
+    got[1] = (uint32_t)__shfl_xor((int)give[1], 16);
+    const u32x4 out = odd ? u32x4{got[0], got[1], keep[0], keep[1]} : u32x4{keep[0], keep[1], got[0], got[1]};
+    float* sg = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (int64_t)(kP * N);
+    *reinterpret_cast<u32x4*>(sg + srow + 16 * N * q) = out;
+  };
+
+  frag8<T> bt[kKS];
+  {
+    const frag8<T>* bf = btf_of(0);
+#pragma unroll
+    for (int ks = 0; ks < kKS; ++ks) bt[ks] = bf[ks * 64];
+  }
+#pragma unroll
+  for (int m = 0; m < kXBlocks / kNW; ++m) issue_copy_part(0, 0, m);
+  dma_wait();
+  __syncthreads();
+  tabulate(0);
+  __syncthreads();
+
+  for (int c = 0; c < p.nchunks; ++c) {
+    const int bc = c & 1, bn = bc ^ 1;
+    const bool has_next = c + 1 < p.nchunks;
+    const float dec = sp.decay[(int64_t)bh * p.nchunks + c];
+    const frag8<T>* bnext = btf_of(has_next ? c + 1 : c);
+    const T* xb = xr[bc];
+    f32x4 acc[PTW];
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) acc[q] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < kKS; ++ks) {
+      set_prio(3 - ks / 2);
+      if (ks < PTW) store_sin(c, ks);
+      if (ks < kXBlocks / kNW && has_next) issue_copy_part(c + 1, bn, ks);
+      const f32x4 w0 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 4 * g);
+      const f32x4 w1 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 16 + 4 * g);
+      frag8<T> hi, lo;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float v = to_f32<T>(bt[ks][j]) * (j < 4 ? w0[j] : w1[j - 4]);
+        hi[j] = from_f32<T>(v);
+        lo[j] = from_f32<T>(v - to_f32<T>(hi[j]));
+      }
+      bt[ks] = bnext[ks * 64];  // (the last chunk reloads its own: no branch, no register copies)
+#pragma unroll
+      for (int q = 0; q < PTW; ++q) {
+        const T* a0 = xb + xoff[q] + (32 * ks) * kP;
+        const frag8<T> xfr = join<T>(lds_read_tr(a0), lds_read_tr(a0 + 16 * kP));
+        acc[q] = mma(hi, xfr, acc[q]);
+        acc[q] = mma(lo, xfr, acc[q]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) st[q] = st[q] * dec + acc[q];
+    // the next chunk's copies were issued before the B^T loads of K steps
+    // 4..7 (the only vector memory operations after them): they have landed
+    // once at most those 4 are outstanding
+    vm_wait<kKS - kXBlocks / kNW>();
+    __syncthreads();
+    if (has_next) tabulate(bn);
+    __syncthreads();
+  }
+  if (sp.final_state) {
+#pragma unroll
+    for (int q = 0; q < PTW; ++q)
+      *reinterpret_cast<f32x4*>(sp.final_state + (int64_t)bh * (kP * N) + srow + 16 * N * q) = st[q];
+  }
+}
+
+template <typename T, int NK>
+hipError_t launch_chain_nk(const ChunkStateArgs& a, const StatePassingArgs& sp, hipStream_t stream) {
+  auto kern = a.dt ? chunk_state_chain_kernel<T, NK, true> : chunk_state_chain_kernel<T, NK, false>;
+  kern<<<dim3((unsigned)(a.batch * a.nheads)), dim3(64 * kNW), 0, stream>>>(a, sp);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 bool chunk_state_persistent_supported(const ChunkStateArgs& a, int dtype) {
@@ -300,6 +483,33 @@ hipError_t launch_chunk_state_persistent(const ChunkStateArgs& a, int dtype, int
     if (dtype == SSD_DTYPE_F16) return launch_ts<f16, bf16>(a, stream);
   }
   return hipErrorInvalidValue;
+}
+
+bool chunk_state_chain_supported(const ChunkStateArgs& a, int dtype) {
+  return chunk_state_persistent_supported(a, dtype) && a.btf != nullptr;
+}
+
+bool chunk_state_chain_preferred(const ChunkStateArgs& a, int dtype) {
+  if (!chunk_state_chain_supported(a, dtype)) return false;
+  // One workgroup per chain, up to two per CU.  The launch saves K3's pass
+  // over the states, but a CU holding two chains runs each at about half
+  // speed: when a fraction of the CUs hold one more chain than the rest (320
+  // chains on 256 CUs), those CUs set the time and K2's independent (b, c, h)
+  // items, then K3, finish first.  Measured on MI355X (forward, chunk 256):
+  // 7-14% faster at 240-1280 chains except 320 chains on 256 CUs (5% slower
+  // at L = 4096).
+  const int64_t chains = (int64_t)a.batch * a.nheads;
+  const int n = device_cu_count();
+  const int64_t cus = n > 0 ? n : 256;
+  const int64_t per_cu = (chains + cus - 1) / cus;
+  return chains <= cus || chains * 5 >= per_cu * cus * 4;
+}
+
+hipError_t launch_chunk_state_chain(const ChunkStateArgs& a, const StatePassingArgs& sp, int dtype,
+                                    hipStream_t stream) {
+  if (!chunk_state_chain_supported(a, dtype) || sp.split_dtype != dtype) return hipErrorInvalidValue;
+  if (dtype == SSD_DTYPE_BF16) return a.dstate == 64 ? launch_chain_nk<bf16, 2>(a, sp, stream) : launch_chain_nk<bf16, 4>(a, sp, stream);
+  return a.dstate == 64 ? launch_chain_nk<f16, 2>(a, sp, stream) : launch_chain_nk<f16, 4>(a, sp, stream);
 }
 
 }  // namespace ssd

@@ -158,6 +158,19 @@ hipError_t launch_chunk_scan(const ChunkScanArgs& a, int dtype, int state_dtype,
 bool chunk_state_persistent_supported(const ChunkStateArgs& a, int dtype);
 hipError_t launch_chunk_state_persistent(const ChunkStateArgs& a, int dtype, int state_dtype, hipStream_t stream);
 
+// K2 and K3 of the chunk-256 forward in one launch (ssd_chunk_state_q256.hip):
+// one workgroup per (b, h) walks the chunks in order with the running state
+// in registers and writes S_in as chunk_scan's hi/lo pairs (sp.split_dtype ==
+// dtype); the per-chunk local states never reach memory.  Needs chunk_prep's
+// B^T fragments (a.btf).  Bit-identical to launch_chunk_state with f32 states
+// followed by launch_state_passing.
+bool chunk_state_chain_supported(const ChunkStateArgs& a, int dtype);
+// ... and faster than the two launches on the current device for this shape
+// (the chains spread evenly over the CUs).
+bool chunk_state_chain_preferred(const ChunkStateArgs& a, int dtype);
+hipError_t launch_chunk_state_chain(const ChunkStateArgs& a, const StatePassingArgs& sp, int dtype,
+                                    hipStream_t stream);
+
 // chunk_scan's persistent kernel for 16-bit inputs at chunk 256
 // (ssd_chunk_scan_q256.hip); launch_chunk_scan dispatches to it when supported.
 bool chunk_scan_persistent_supported(const ChunkScanArgs& a, int dtype);
