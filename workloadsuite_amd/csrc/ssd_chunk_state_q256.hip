@@ -492,17 +492,18 @@ bool chunk_state_chain_supported(const ChunkStateArgs& a, int dtype) {
 bool chunk_state_chain_preferred(const ChunkStateArgs& a, int dtype) {
   if (!chunk_state_chain_supported(a, dtype)) return false;
   // One workgroup per chain, up to two per CU.  The launch saves K3's pass
-  // over the states, but a CU holding two chains runs each at about half
-  // speed: when a fraction of the CUs hold one more chain than the rest (320
-  // chains on 256 CUs), those CUs set the time and K2's independent (b, c, h)
-  // items, then K3, finish first.  Measured on MI355X (forward, chunk 256):
-  // 7-14% faster at 240-1280 chains except 320 chains on 256 CUs (5% slower
-  // at L = 4096).
+  // over the states but runs each chain's chunks in sequence: it pays off
+  // only when the chains keep every CU equally busy.  With fewer chains than
+  // CUs the idle CUs are lost (C4, 80 chains of 256 chunks: 31% slower), and
+  // with a fraction of the CUs holding one more chain than the rest (320
+  // chains on 256 CUs) those CUs set the time.  Measured on MI355X (forward,
+  // chunk 256): 7-14% faster wherever the average CU holds at least 3/4 of
+  // the busiest CU's chains, up to 8% slower elsewhere down to 128 chains.
   const int64_t chains = (int64_t)a.batch * a.nheads;
   const int n = device_cu_count();
   const int64_t cus = n > 0 ? n : 256;
   const int64_t per_cu = (chains + cus - 1) / cus;
-  return chains <= cus || chains * 5 >= per_cu * cus * 4;
+  return 4 * chains >= 3 * per_cu * cus;
 }
 
 hipError_t launch_chunk_state_chain(const ChunkStateArgs& a, const StatePassingArgs& sp, int dtype,
