@@ -5,8 +5,9 @@
                     [--state-dtype f32|bf16] [--no-cpu-baseline]
     python bench.py --layer [--steps K] [--warmup W]
 
-A step is one SSD forward (K1 cumsum -> K0 chunk_prep -> K2 chunk_state ->
-K3 state_passing -> K4 chunk_scan) over one batch of synthetic inputs already resident in HBM, at
+A step is one SSD forward (K1 cumsum and K0 chunk_prep in one launch -> K2
+chunk_state and K3 state_passing, one launch per (b, h) chain where that is
+faster -> K4 chunk_scan) over one batch of synthetic inputs already resident in HBM, at
 the Mamba-2-2.7B layer shape by default (C3: batch 4, seqlen 4096, 80 heads,
 head_dim 64, d_state 128, chunk 256, 1 group, bf16 X/B/C, fp32 A, final state
 returned).  Prints ONE JSON line.
@@ -82,6 +83,8 @@ def kernel_model(cfg, state_dtype):
         "chunk_prep": dict(bytes=2 * bc + cb_frag + bt_frag, flops=2 * b * c * g * TQ * N),
         "chunk_state": dict(bytes=x + bc + acs + st, flops=2 * b * c * h * Q * P * N),
         "state_passing": dict(bytes=2 * st + dec + fin + init, flops=2 * b * c * h * P * N),
+        # K2 + K3 as the forward runs them: x in, S_in out; the local states are not counted
+        "chunk_state_passing": dict(bytes=x + bc + acs + dec + st + fin + init, flops=2 * b * c * h * (Q + 1) * P * N),
         "chunk_scan": dict(bytes=x + 2 * bc + acs + st + x,
                            flops=b * c * h * (2 * TQ * N + 2 * TQ * P + 2 * Q * N * P)),
     }
@@ -303,6 +306,9 @@ def main():
         "chunk_prep": lambda: S.chunk_prep(B, C, cfg.chunk),
         "chunk_state": lambda: S.chunk_state(X, B, Acs, state_dtype=state_dtype, prep=prep),
         "state_passing": lambda: S.state_passing_(sp_buf, decay, init, sp_final, split=split),
+        "chunk_state_passing": lambda: S.chunk_state_passing(X, B, Acs, decay, prep=prep, initial_states=init,
+                                                             return_final_states=cfg.final_state, split=split,
+                                                             state_dtype=state_dtype),
         "chunk_scan": lambda: S.chunk_scan(X, B, C, Acs, S_in, prep=prep, split=split is not None),
     }
     if prep is None:

@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SSD_ABI_VERSION 3
+#define SSD_ABI_VERSION 4
 
 /* Element types.  The two SPLIT values are a storage format of the per-chunk
  * states only: each f32 state as the 16-bit pair hi = round(v),
@@ -145,6 +145,25 @@ int ssd_chunk_state(const ssd_dims* d, int dtype,
 int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype,
                       const float* chunk_decay, const float* initial_states,
                       float* final_states, void* stream);
+
+/* K2 then K3 as ssd_forward runs them: on return states holds S_in (the
+ * state entering each chunk, [b, c, h, P, N]) in state_dtype, exactly as
+ * ssd_chunk_state (f32 local states for the SPLIT formats, else state_dtype)
+ * followed by ssd_state_passing would leave it.  For a SPLIT state_dtype of
+ * the inputs' type with prep (chunk 256), the two stages run as one launch
+ * wherever that is faster on the device: each (b, h) chain of chunks keeps
+ * its running state in registers and the local states are never stored.
+ * Replaces MR:144-157 (X*dt, decay_to_end, block_state, the state loop).
+ * a_cumsum, chunk_decay: ssd_chunk_cumsum's outputs; prep as for
+ * ssd_chunk_state; initial_states / final_states as for ssd_state_passing. */
+int ssd_chunk_state_passing(const ssd_dims* d, int dtype,
+                            const void* x, const int64_t x_strides[4],
+                            const void* bmat, const int64_t b_strides[4],
+                            const float* dt, const int64_t dt_strides[3],
+                            const float* a_cumsum, const float* chunk_decay,
+                            const void* prep, const float* initial_states,
+                            void* states, int state_dtype, float* final_states,
+                            void* stream);
 
 /* Skip and gate of SSDLayer.forward (MR:116-118), applied by ssd_chunk_scan
  * to y in float32 before its single rounding to the output dtype:

@@ -2,8 +2,10 @@
 (each workgroup walks one (batch, head) chain of chunks with the running
 state in registers, workloads/mamba/model_ref.py:144-157) when the chains
 keep every CU about equally busy: at least 3/4 of the busiest CU's chains on
-the average CU.  The shapes here have 192-256 chains (one per CU on a 256-CU
-MI355X) or 640 (three per CU), so they take that launch.  It must give exactly what the two kernels
+the average CU.  Between one and two chains per CU it runs one whole chain
+per CU and the remaining chains in segments whose local states
+state_passing finishes.  The shapes here have 192-256 chains (one per CU on
+a 256-CU MI355X), 640 (three per CU) or 300-360 (the mixed plan).  It must give exactly what the two kernels
 give one after the other: ssd_forward against the public per-kernel entry
 points, bit for bit (Y and the final state), with and without dt and an
 initial state, both 16-bit types, both dstates, several groups.  The
@@ -19,11 +21,22 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def takes_chain(chains):
-    """The library's dispatch rule (chunk_state_chain_preferred) on this device."""
+def chain_plan(chains):
+    """The library's dispatch rule (chunk_state_chain_plan) on this device:
+    "whole" (every chain in one workgroup), "mixed" (one whole chain per CU,
+    the rest in segments finished by state_passing) or None (chunk_state then
+    state_passing)."""
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     per_cu = -(-chains // cus)
-    return 4 * chains >= 3 * per_cu * cus
+    if 4 * chains >= 3 * per_cu * cus:
+        return "whole"
+    if cus < chains < 2 * cus:
+        return "mixed"
+    return None
+
+
+def takes_chain(chains):
+    return chain_plan(chains) is not None
 
 
 def case(dtype, b, L, h, P, N, g, seed):
@@ -77,3 +90,42 @@ def test_single_chunk_and_many_chains():
         torch.cuda.synchronize()
         assert torch.equal(final, fk)
         assert torch.equal(Y, Yk)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("b,h,L,g", [(2, 160, 1280, 1), (3, 120, 2048, 4), (1, 300, 256, 2), (2, 150, 4096, 2)])
+def test_mixed_plan_equals_kernels_one_by_one(dtype, b, h, L, g):
+    """Whole chains, segments of the remaining chains (ragged last segment
+    with 5 chunks, a single chunk, 16 chunks), state_passing over those
+    chains only, with an initial state and the final state."""
+    print("CASE chain mixed", dtype, b, h, L, g, flush=True)
+    if chain_plan(b * h) != "mixed":
+        pytest.skip("this device's CU count does not give the mixed plan for this shape")
+    X, A, B, C, dt, init = case(dtype, b, L, h, 64, 128, g, seed=b * h + L)
+    Y, final = S.ssd_forward(X, A, B, C, 256, dt=dt, initial_states=init, return_final_states=True)
+    Acs, decay = S.chunk_cumsum(A, 256)
+    prep = S.chunk_prep(B, C, 256)
+    st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
+    S_in, fk = S.state_passing(st, decay, initial_states=init, split=dtype)
+    Yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dt, prep=prep, split=True)
+    torch.cuda.synchronize()
+    assert torch.equal(final, fk)
+    assert torch.equal(Y, Yk)
+
+
+@pytest.mark.parametrize("b,h,L", [(2, 128, 1280), (2, 160, 1280), (1, 24, 512)])
+@pytest.mark.parametrize("split", [torch.bfloat16, None])
+def test_chunk_state_passing_entry_point(b, h, L, split):
+    """ssd_chunk_state_passing (whole chains, the mixed plan, or chunk_state
+    then state_passing, by shape) against the two entry points it stands for,
+    bit for bit; also without split (f32 S_in, always two launches)."""
+    print("CASE chunk_state_passing", b, h, L, split, flush=True)
+    X, A, B, C, dt, init = case(torch.bfloat16, b, L, h, 64, 128, 2, seed=h + L)
+    Acs, decay = S.chunk_cumsum(A, 256)
+    prep = S.chunk_prep(B, C, 256)
+    S_in, final = S.chunk_state_passing(X, B, Acs, decay, dt=dt, prep=prep, initial_states=init, split=split)
+    st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
+    S_ref, f_ref = S.state_passing(st, decay, initial_states=init, split=split)
+    torch.cuda.synchronize()
+    assert torch.equal(final, f_ref)
+    assert torch.equal(S_in.view(torch.uint8), S_ref.view(torch.uint8))

@@ -8,8 +8,9 @@ Kernels live in ``libssd.so`` (built by ``python -m workloadsuite_amd.build``);
 the C ABI is ``include/ssd.h``.
 """
 
-from .ssd import (SSDError, chunk_cumsum, chunk_prep, chunk_scan, chunk_state, decode_step, layer_prep, ssd_core,
-                  ssd_forward, ssd_layer, state_passing, workspace_bytes)
+from .ssd import (SSDError, chunk_cumsum, chunk_prep, chunk_scan, chunk_state, chunk_state_passing, decode_step,
+                  layer_prep, ssd_core, ssd_forward, ssd_layer, state_passing, workspace_bytes)
 
-__all__ = ["ssd_forward", "ssd_core", "chunk_cumsum", "chunk_prep", "chunk_state", "state_passing", "chunk_scan",
+__all__ = ["ssd_forward", "ssd_core", "chunk_cumsum", "chunk_prep", "chunk_state", "state_passing",
+           "chunk_state_passing", "chunk_scan",
            "decode_step", "layer_prep", "ssd_layer", "workspace_bytes", "SSDError"]

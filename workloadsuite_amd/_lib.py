@@ -15,7 +15,7 @@ import torch  # noqa: F401  -- must precede the CDLL, see module docstring
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssd.so")
 
-SSD_ABI_VERSION = 3
+SSD_ABI_VERSION = 4
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 STATE_SPLIT_BF16, STATE_SPLIT_F16 = 3, 4  # f32 states as 16-bit (hi, lo) pairs
 
@@ -30,6 +30,7 @@ EXPORTS = (
     "ssd_chunk_cumsum",
     "ssd_chunk_state",
     "ssd_state_passing",
+    "ssd_chunk_state_passing",
     "ssd_chunk_scan",
     "ssd_forward",
     "ssd_decode_step",
@@ -70,6 +71,8 @@ _SIGNATURES = {
     "ssd_chunk_prep": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, ctypes.c_size_t, _vp]),
     "ssd_chunk_state": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _int, _vp, _vp]),
     "ssd_state_passing": (_int, [_dims_p, _vp, _int, _vp, _vp, _vp, _vp]),
+    "ssd_chunk_state_passing": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _vp, _vp,
+                                       _vp, _int, _vp, _vp]),
     "ssd_chunk_scan": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                               _vp, _vp, _int, _vp, _i64p, _vp, _epi_p, _vp]),
     "ssd_forward": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,

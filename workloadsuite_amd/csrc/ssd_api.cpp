@@ -285,6 +285,29 @@ CumsumArgs make_cumsum_args(const ssd_dims* d, const float* a, const int64_t a_s
 // K1 (when k1 is given; together with K0 in one launch where K0 applies), K0,
 // K2, K3, K4 of one forward.  Without k1, K1's outputs are already in the
 // workspace.  Operands are validated by the caller.
+// K2 then K3 (local states in the f32 / bf16 state_dtype; pa.split_dtype set:
+// S_in written as hi/lo pairs), as one chain launch where that is faster.
+int run_state_passing(const ssd_dims* d, int dtype, const ChunkStateArgs& sa, const StatePassingArgs& pa,
+                      int state_dtype, hipStream_t s) {
+  int rc;
+  const ssd::ChainPlan plan = pa.split_dtype ? ssd::chunk_state_chain_plan(sa, dtype) : ssd::ChainPlan{0, 1, 1};
+  if (plan.nfull > 0) {
+    // K2 and K3 as one launch: the local states stay in registers (same bits);
+    // chains beyond nfull leave local states that K3 finishes
+    if ((rc = hip_status(ssd::launch_chunk_state_chain(sa, pa, plan, dtype, s)))) return rc;
+    const int64_t chains = d->batch * d->nheads;
+    if (plan.nfull < chains) {
+      StatePassingArgs rest = pa;
+      rest.bh_begin = plan.nfull;
+      rest.bh_count = (int)(chains - plan.nfull);
+      if ((rc = hip_status(ssd::launch_state_passing(rest, state_dtype, s)))) return rc;
+    }
+    return SSD_OK;
+  }
+  if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, state_dtype, s)))) return rc;
+  return hip_status(ssd::launch_state_passing(pa, state_dtype, s));
+}
+
 int run_core(const ssd_dims* d, int dtype, const CumsumArgs* k1, const void* x, const int64_t x_strides[4],
              const void* bmat, const int64_t b_strides[4], const void* cmat, const int64_t c_strides[4],
              const float* dt, const int64_t dt_strides[3], const float* initial_states, void* y,
@@ -319,13 +342,7 @@ int run_core(const ssd_dims* d, int dtype, const CumsumArgs* k1, const void* x, 
     pa.split_dtype = dtype;
     ca.presplit = true;
   }
-  if (pa.split_dtype && ssd::chunk_state_chain_preferred(sa, dtype)) {
-    // K2 and K3 as one launch: the local states stay in registers (same bits)
-    if ((rc = hip_status(ssd::launch_chunk_state_chain(sa, pa, dtype, s)))) return rc;
-  } else {
-    if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, state_dtype, s)))) return rc;
-    if ((rc = hip_status(ssd::launch_state_passing(pa, state_dtype, s)))) return rc;
-  }
+  if ((rc = run_state_passing(d, dtype, sa, pa, state_dtype, s))) return rc;
   return hip_status(ssd::launch_chunk_scan(ca, dtype, state_dtype, s));
 }
 
@@ -551,6 +568,30 @@ int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, const fl
   StatePassingArgs p = make_sp_args(d, states, chunk_decay, initial_states, final_states);
   p.split_dtype = split;
   return hip_status(ssd::launch_state_passing(p, split ? SSD_DTYPE_F32 : state_dtype, (hipStream_t)stream));
+}
+
+int ssd_chunk_state_passing(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4],
+                            const void* bmat, const int64_t b_strides[4], const float* dt,
+                            const int64_t dt_strides[3], const float* a_cumsum, const float* chunk_decay,
+                            const void* prep, const float* initial_states, void* states, int state_dtype,
+                            float* final_states, void* stream) {
+  int rc = check_dims_impl(d, dtype);
+  if (rc) return rc;
+  const int split = split_of(state_dtype);
+  if (split ? split != dtype : !valid_state_dtype(dtype, state_dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+  if ((rc = check_vec_operand(x, x_strides, 4, dtype))) return rc;
+  if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
+  if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
+  if (!a_cumsum || !chunk_decay || !states) return SSD_ERR_NULL_POINTER;
+  if (!aligned16(states) || (initial_states && !aligned16(initial_states)) ||
+      (final_states && !aligned16(final_states)))
+    return SSD_ERR_MISALIGNED;
+  if (prep && (reinterpret_cast<uintptr_t>(prep) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
+  ChunkStateArgs sa = make_state_args(d, x, x_strides, bmat, b_strides, dt, dt_strides, a_cumsum, states);
+  if (prep_applies(d, dtype)) sa.btf = prep_btf(d, prep);
+  StatePassingArgs pa = make_sp_args(d, states, chunk_decay, initial_states, final_states);
+  pa.split_dtype = split;
+  return run_state_passing(d, dtype, sa, pa, split ? SSD_DTYPE_F32 : state_dtype, (hipStream_t)stream);
 }
 
 int ssd_chunk_scan(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4],

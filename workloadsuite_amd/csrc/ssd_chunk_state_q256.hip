@@ -25,6 +25,8 @@
 //
 // Traffic per item: x 32 KB + Acs 1 KB read, states 32 KB (f32) written; B
 // once per group.  HBM bound at this shape.
+#include <climits>
+
 #include "ssd_device.h"
 #include "ssd_launch.h"
 #include "../../include/ssd.h"
@@ -304,9 +306,16 @@ hipError_t launch_ts(const ChunkStateArgs& a, hipStream_t stream) {
 // the next chunk is loaded into its register as soon as the current chunk's
 // weighting has consumed it, so the per-chunk group operands arrive under
 // the current chunk's compute.
+//
+// Workgroups [0, plan.nfull) walk the whole chains bh = blockIdx.  Each of
+// the rest takes plan.seg_len chunks of one of the remaining chains (chains
+// nfull, nfull + 1, ...; plan.seg_per_chain segments each) and writes those
+// chunks' f32 local states, exactly as chunk_state would, for state_passing
+// to finish: with 1.25 chains per CU the whole chains take one workgroup slot
+// of every CU and the segments the second.
 template <typename T, int NK, bool HAS_DT>
 __global__ __launch_bounds__(64 * kNW) __attribute__((amdgpu_waves_per_eu(4)))
-void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp) {
+void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan plan) {
   constexpr int N = 32 * NK;
   constexpr int NTILE = N / 16;
   constexpr int PTW = NTILE / 2;
@@ -320,7 +329,15 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   __builtin_assume(wave < kNW);
   const int g = lane >> 4, i = lane & 15;
-  const int bh = blockIdx.x;  // b * nheads + h
+  const bool local = (int)blockIdx.x >= plan.nfull;  // workgroup-uniform
+  int bh = blockIdx.x, c0 = 0, c1 = p.nchunks;     // chain b * nheads + h, chunks [c0, c1)
+  if (local) {
+    const int sg = (int)blockIdx.x - plan.nfull;
+    bh = plan.nfull + sg / plan.seg_per_chain;
+    c0 = (sg % plan.seg_per_chain) * plan.seg_len;
+    c1 = min(c0 + plan.seg_len, p.nchunks);
+    if (c0 >= c1) return;  // the whole workgroup, before any barrier
+  }
   const int h = bh % p.nheads, b = bh / p.nheads;
   const int grp = h / (p.nheads / p.ngroups);
   const int nt = wave % NTILE, pt0 = (wave / NTILE) * PTW;
@@ -372,8 +389,8 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp) {
   f32x4 st[PTW];
 #pragma unroll
   for (int q = 0; q < PTW; ++q)
-    st[q] = sp.init ? *reinterpret_cast<const f32x4*>(sp.init + (int64_t)bh * (kP * N) + srow + 16 * N * q)
-                    : f32x4{0.f, 0.f, 0.f, 0.f};
+    st[q] = sp.init && !local ? *reinterpret_cast<const f32x4*>(sp.init + (int64_t)bh * (kP * N) + srow + 16 * N * q)
+                              : f32x4{0.f, 0.f, 0.f, 0.f};
 
   // S_in of chunk c, as [hi x8 | lo x8] of T per 8 consecutive states: lane
   // pairs (g, g ^ 1) swap halves so that the even-g lane stores the 8 hi and
@@ -396,23 +413,28 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp) {
     float* sg = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (int64_t)(kP * N);
     *reinterpret_cast<u32x4*>(sg + srow + 16 * N * q) = out;
   };
+  // a segment's local state of chunk c (f32, chunk_state's layout)
+  auto store_local = [&](int c, int q) __attribute__((always_inline)) {
+    float* sg = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (int64_t)(kP * N);
+    *reinterpret_cast<f32x4*>(sg + srow + 16 * N * q) = st[q];
+  };
 
   frag8<T> bt[kKS];
   {
-    const frag8<T>* bf = btf_of(0);
+    const frag8<T>* bf = btf_of(c0);
 #pragma unroll
     for (int ks = 0; ks < kKS; ++ks) bt[ks] = bf[ks * 64];
   }
 #pragma unroll
-  for (int m = 0; m < kXBlocks / kNW; ++m) issue_copy_part(0, 0, m);
+  for (int m = 0; m < kXBlocks / kNW; ++m) issue_copy_part(c0, 0, m);
   dma_wait();
   __syncthreads();
   tabulate(0);
   __syncthreads();
 
-  for (int c = 0; c < p.nchunks; ++c) {
-    const int bc = c & 1, bn = bc ^ 1;
-    const bool has_next = c + 1 < p.nchunks;
+  for (int c = c0; c < c1; ++c) {
+    const int bc = (c - c0) & 1, bn = bc ^ 1;
+    const bool has_next = c + 1 < c1;
     const float dec = sp.decay[(int64_t)bh * p.nchunks + c];
     const frag8<T>* bnext = btf_of(has_next ? c + 1 : c);
     const T* xb = xr[bc];
@@ -422,7 +444,10 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp) {
 #pragma unroll
     for (int ks = 0; ks < kKS; ++ks) {
       set_prio(3 - ks / 2);
-      if (ks < PTW) store_sin(c, ks);
+      if (ks < PTW) {
+        if (!local) store_sin(c, ks);
+        else if (c > c0) store_local(c - 1, ks);  // st holds chunk c - 1's local state
+      }
       if (ks < kXBlocks / kNW && has_next) issue_copy_part(c + 1, bn, ks);
       const f32x4 w0 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 4 * g);
       const f32x4 w1 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 16 + 4 * g);
@@ -444,7 +469,7 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp) {
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int q = 0; q < PTW; ++q) st[q] = st[q] * dec + acc[q];
+    for (int q = 0; q < PTW; ++q) st[q] = local ? acc[q] : st[q] * dec + acc[q];
     // the next chunk's copies were issued before the B^T loads of K steps
     // 4..7 (the only vector memory operations after them): they have landed
     // once at most those 4 are outstanding
@@ -453,7 +478,10 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp) {
     if (has_next) tabulate(bn);
     __syncthreads();
   }
-  if (sp.final_state) {
+  if (local) {
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) store_local(c1 - 1, q);
+  } else if (sp.final_state) {
 #pragma unroll
     for (int q = 0; q < PTW; ++q)
       *reinterpret_cast<f32x4*>(sp.final_state + (int64_t)bh * (kP * N) + srow + 16 * N * q) = st[q];
@@ -461,9 +489,12 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp) {
 }
 
 template <typename T, int NK>
-hipError_t launch_chain_nk(const ChunkStateArgs& a, const StatePassingArgs& sp, hipStream_t stream) {
+hipError_t launch_chain_nk(const ChunkStateArgs& a, const StatePassingArgs& sp, const ChainPlan& plan,
+                           hipStream_t stream) {
   auto kern = a.dt ? chunk_state_chain_kernel<T, NK, true> : chunk_state_chain_kernel<T, NK, false>;
-  kern<<<dim3((unsigned)(a.batch * a.nheads)), dim3(64 * kNW), 0, stream>>>(a, sp);
+  const int64_t rest = (int64_t)a.batch * a.nheads - plan.nfull;
+  const unsigned grid = (unsigned)(plan.nfull + rest * plan.seg_per_chain);
+  kern<<<dim3(grid), dim3(64 * kNW), 0, stream>>>(a, sp, plan);
   return hipGetLastError();
 }
 
@@ -489,28 +520,44 @@ bool chunk_state_chain_supported(const ChunkStateArgs& a, int dtype) {
   return chunk_state_persistent_supported(a, dtype) && a.btf != nullptr;
 }
 
-bool chunk_state_chain_preferred(const ChunkStateArgs& a, int dtype) {
-  if (!chunk_state_chain_supported(a, dtype)) return false;
+ChainPlan chunk_state_chain_plan(const ChunkStateArgs& a, int dtype) {
+  ChainPlan none{0, 1, 1};
+  if (!chunk_state_chain_supported(a, dtype)) return none;
   // One workgroup per chain, up to two per CU.  The launch saves K3's pass
-  // over the states but runs each chain's chunks in sequence: it pays off
+  // over the states but runs each chain's chunks in sequence, so it pays off
   // only when the chains keep every CU equally busy.  With fewer chains than
-  // CUs the idle CUs are lost (C4, 80 chains of 256 chunks: 31% slower), and
-  // with a fraction of the CUs holding one more chain than the rest (320
-  // chains on 256 CUs) those CUs set the time.  Measured on MI355X (forward,
-  // chunk 256): 7-14% faster wherever the average CU holds at least 3/4 of
-  // the busiest CU's chains, up to 8% slower elsewhere down to 128 chains.
+  // CUs the idle CUs are lost (C4, 80 chains of 256 chunks: 31% slower than
+  // K2 then K3).  Measured on MI355X (forward, chunk 256): 7-14% faster
+  // wherever the average CU holds at least 3/4 of the busiest CU's chains.
   const int64_t chains = (int64_t)a.batch * a.nheads;
   const int n = device_cu_count();
   const int64_t cus = n > 0 ? n : 256;
   const int64_t per_cu = (chains + cus - 1) / cus;
-  return 4 * chains >= 3 * per_cu * cus;
+  if (4 * chains >= 3 * per_cu * cus) return ChainPlan{(int)chains, 1, a.nchunks};
+  // Between one and two chains per CU (C3: 320 chains on 256 CUs) the CUs
+  // holding a second chain would set the time.  One whole chain per CU, and
+  // the remaining chains in segments that fill the second slots; their local
+  // states go to state_passing, which then runs over those chains only.
+  if (chains > cus && chains < 2 * cus) {
+    const int64_t rest = chains - cus;
+    const int64_t want = cus / rest > 1 ? cus / rest : 1;  // segments per chain
+    const int seg_len = (int)((a.nchunks + want - 1) / want);
+    const int segs = (a.nchunks + seg_len - 1) / seg_len;
+    return ChainPlan{(int)cus, segs, seg_len};
+  }
+  return none;
 }
 
-hipError_t launch_chunk_state_chain(const ChunkStateArgs& a, const StatePassingArgs& sp, int dtype,
-                                    hipStream_t stream) {
-  if (!chunk_state_chain_supported(a, dtype) || sp.split_dtype != dtype) return hipErrorInvalidValue;
-  if (dtype == SSD_DTYPE_BF16) return a.dstate == 64 ? launch_chain_nk<bf16, 2>(a, sp, stream) : launch_chain_nk<bf16, 4>(a, sp, stream);
-  return a.dstate == 64 ? launch_chain_nk<f16, 2>(a, sp, stream) : launch_chain_nk<f16, 4>(a, sp, stream);
+hipError_t launch_chunk_state_chain(const ChunkStateArgs& a, const StatePassingArgs& sp, const ChainPlan& plan,
+                                    int dtype, hipStream_t stream) {
+  const int64_t chains = (int64_t)a.batch * a.nheads;
+  if (!chunk_state_chain_supported(a, dtype) || sp.split_dtype != dtype || plan.nfull < 1 || plan.nfull > chains ||
+      plan.seg_per_chain < 1 || plan.seg_len < 1 || (int64_t)plan.seg_per_chain * plan.seg_len < a.nchunks ||
+      plan.nfull + (chains - plan.nfull) * plan.seg_per_chain > INT_MAX)
+    return hipErrorInvalidValue;
+  if (dtype == SSD_DTYPE_BF16)
+    return a.dstate == 64 ? launch_chain_nk<bf16, 2>(a, sp, plan, stream) : launch_chain_nk<bf16, 4>(a, sp, plan, stream);
+  return a.dstate == 64 ? launch_chain_nk<f16, 2>(a, sp, plan, stream) : launch_chain_nk<f16, 4>(a, sp, plan, stream);
 }
 
 }  // namespace ssd

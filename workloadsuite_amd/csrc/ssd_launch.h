@@ -61,6 +61,8 @@ struct StatePassingArgs {
   // 0, or SSD_DTYPE_BF16 / F16: f32 S_in is written as chunk_scan's hi/lo
   // operand pairs of that type (chunk-256 forward path only)
   int split_dtype = 0;
+  // chains (b * nheads + h) [bh_begin, bh_begin + bh_count) only; bh_count 0: all
+  int bh_begin = 0, bh_count = 0;
 };
 
 struct ChunkScanArgs {
@@ -159,17 +161,23 @@ bool chunk_state_persistent_supported(const ChunkStateArgs& a, int dtype);
 hipError_t launch_chunk_state_persistent(const ChunkStateArgs& a, int dtype, int state_dtype, hipStream_t stream);
 
 // K2 and K3 of the chunk-256 forward in one launch (ssd_chunk_state_q256.hip):
-// one workgroup per (b, h) walks the chunks in order with the running state
-// in registers and writes S_in as chunk_scan's hi/lo pairs (sp.split_dtype ==
+// one workgroup per (b, h) chain walks the chunks in order with the running
+// state in registers and writes S_in as chunk_scan's hi/lo pairs (sp.split_dtype ==
 // dtype); the per-chunk local states never reach memory.  Needs chunk_prep's
 // B^T fragments (a.btf).  Bit-identical to launch_chunk_state with f32 states
 // followed by launch_state_passing.
 bool chunk_state_chain_supported(const ChunkStateArgs& a, int dtype);
-// ... and faster than the two launches on the current device for this shape
-// (the chains spread evenly over the CUs).
-bool chunk_state_chain_preferred(const ChunkStateArgs& a, int dtype);
-hipError_t launch_chunk_state_chain(const ChunkStateArgs& a, const StatePassingArgs& sp, int dtype,
-                                    hipStream_t stream);
+// Chains [0, nfull) run whole; each later chain runs as seg_per_chain
+// workgroups of seg_len chunks that write f32 local states, and
+// launch_state_passing over chains [nfull, b*h) (bh_begin / bh_count) then
+// finishes them.  nfull == 0: the launch is not worth it on this device for
+// this shape; run launch_chunk_state then launch_state_passing instead.
+struct ChainPlan {
+  int nfull, seg_per_chain, seg_len;
+};
+ChainPlan chunk_state_chain_plan(const ChunkStateArgs& a, int dtype);
+hipError_t launch_chunk_state_chain(const ChunkStateArgs& a, const StatePassingArgs& sp, const ChainPlan& plan,
+                                    int dtype, hipStream_t stream);
 
 // chunk_scan's persistent kernel for 16-bit inputs at chunk 256
 // (ssd_chunk_scan_q256.hip); launch_chunk_scan dispatches to it when supported.

@@ -47,7 +47,7 @@ __global__ __launch_bounds__(256) void state_passing_kernel(StatePassingArgs p) 
   const int64_t PN = (int64_t)p.headdim * p.dstate;
   const int vec_per_bh = (int)(PN / 4);
   const int blocks_per_bh = (vec_per_bh + 255) / 256;
-  const int bh = blockIdx.x / blocks_per_bh;  // b * nheads + h
+  const int bh = p.bh_begin + (int)blockIdx.x / blocks_per_bh;  // b * nheads + h
   const int v = (blockIdx.x % blocks_per_bh) * 256 + threadIdx.x;
   if (v >= vec_per_bh) return;
   const int h = bh % p.nheads, b = bh / p.nheads;
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(256) void state_passing_split_kernel(StatePassingAr
   const int64_t PN = (int64_t)p.headdim * p.dstate;
   const int vec_per_bh = (int)(PN / 4);
   const int blocks_per_bh = (vec_per_bh + 255) / 256;
-  const int bh = blockIdx.x / blocks_per_bh;
+  const int bh = p.bh_begin + (int)blockIdx.x / blocks_per_bh;
   const int v = (blockIdx.x % blocks_per_bh) * 256 + threadIdx.x;
   if (v >= vec_per_bh) return;  // vec_per_bh is a multiple of 256: whole waves leave together
   const int h = bh % p.nheads, b = bh / p.nheads;
@@ -145,17 +145,20 @@ __global__ __launch_bounds__(256) void state_passing_split_kernel(StatePassingAr
 
 hipError_t launch_state_passing(const StatePassingArgs& a, int state_dtype, hipStream_t stream) {
   const int64_t PN = (int64_t)a.headdim * a.dstate;
+  const int64_t all = (int64_t)a.batch * a.nheads;
+  if (a.bh_begin < 0 || a.bh_count < 0 || a.bh_begin + (int64_t)a.bh_count > all) return hipErrorInvalidValue;
+  const int64_t chains = a.bh_count > 0 ? a.bh_count : all - a.bh_begin;
   if (a.split_dtype != 0) {
     if (state_dtype != SSD_DTYPE_F32 || PN % 8 != 0) return hipErrorInvalidValue;
     if (PN % 256 != 0) return hipErrorInvalidValue;  // whole waves per (b, h)
-    const dim3 grid((unsigned)((int64_t)a.batch * a.nheads * ((PN / 4 + 255) / 256)));
+    const dim3 grid((unsigned)(chains * ((PN / 4 + 255) / 256)));
     if (a.split_dtype == SSD_DTYPE_BF16) state_passing_split_kernel<bf16><<<grid, 256, 0, stream>>>(a);
     else if (a.split_dtype == SSD_DTYPE_F16) state_passing_split_kernel<f16><<<grid, 256, 0, stream>>>(a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
   }
   const int64_t blocks_per_bh = (PN / 4 + 255) / 256;
-  const dim3 grid((unsigned)((int64_t)a.batch * a.nheads * blocks_per_bh));
+  const dim3 grid((unsigned)(chains * blocks_per_bh));
   if (state_dtype == SSD_DTYPE_F32) {
     state_passing_kernel<float><<<grid, 256, 0, stream>>>(a);
   } else if (state_dtype == SSD_DTYPE_BF16) {

@@ -298,6 +298,37 @@ def state_passing_(states, chunk_decay, initial_states=None, final_states=None, 
     return states
 
 
+def chunk_state_passing(X, B, Acs, chunk_decay, dt=None, prep=None, initial_states=None,
+                        return_final_states=True, split=None, state_dtype=torch.float32):
+    """K2 then K3 as ``ssd_forward`` runs them (MR:144-157): (S_in [b, c, h, P, N],
+    final [b, h, P, N] or None).  Same values as ``chunk_state`` followed by
+    ``state_passing``; with ``split`` (the inputs' 16-bit type) and ``prep`` at
+    chunk 256 the two run as one launch where that is faster on the device."""
+    b, L, h, P = X.shape
+    g, N = B.shape[2], B.shape[3]
+    Q = Acs.shape[-1]
+    dev = _device_check(X, B, Acs, chunk_decay, dt, initial_states)
+    d = _dims(b, L, h, P, N, g, Q)
+    X, Bm = _vec_operand(X.detach()), _vec_operand(B.detach())
+    Acs = _f32_contig(Acs)
+    decay = _f32_contig(chunk_decay)
+    dt = _f32_operand(dt)
+    init = _f32_contig(initial_states)
+    if split is not None:
+        if split not in _SPLIT_STATES:
+            raise ValueError("split must be torch.bfloat16 or torch.float16")
+        sd, store = _SPLIT_STATES[split], torch.float32
+    else:
+        sd, store = _STATE_DTYPES[state_dtype], state_dtype
+    states = torch.empty((b, L // Q, h, P, N), dtype=store, device=dev)
+    final = torch.empty((b, h, P, N), dtype=torch.float32, device=dev) if return_final_states else None
+    _lib.check(_lib.load().ssd_chunk_state_passing(
+        ctypes.byref(d), _DTYPES[X.dtype], _ptr(X), _lib.strides(X), _ptr(Bm), _lib.strides(Bm),
+        _ptr(dt), _lib.strides(dt) if dt is not None else None, _ptr(Acs), _ptr(decay), _ptr(prep), _ptr(init),
+        _ptr(states), sd, _ptr(final), _stream(dev)))
+    return states, final
+
+
 def _epilogue(X, D, z, dev):
     """The skip / gate epilogue struct (or None) and the tensors it points into."""
     if D is None and z is None:
