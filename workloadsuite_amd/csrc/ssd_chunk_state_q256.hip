@@ -302,10 +302,12 @@ hipError_t launch_ts(const ChunkStateArgs& a, hipStream_t stream) {
 // result is bit-identical.
 //
 // Pipelining per chunk step: the next chunk's x, Acs and dt copies are
-// issued in K steps 0-3 (after the S_in stores), and each B^T fragment of
-// the next chunk is loaded into its register as soon as the current chunk's
-// weighting has consumed it, so the per-chunk group operands arrive under
-// the current chunk's compute.
+// issued in K steps 0-3, and each B^T fragment of the next chunk is loaded
+// into its register as soon as the current chunk's weighting has consumed
+// it, so the per-chunk group operands arrive under the current chunk's
+// compute.  The chunk's S_in stores go out after all of that (storing them
+// at the start of the step instead costs 7-12%: later waits for the B^T
+// fragments then also wait for those stores).
 //
 // Workgroups [0, plan.nfull) walk the whole chains bh = blockIdx.  Each of
 // the rest takes plan.seg_len chunks of one of the remaining chains (chains
@@ -319,7 +321,6 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
   constexpr int N = 32 * NK;
   constexpr int NTILE = N / 16;
   constexpr int PTW = NTILE / 2;
-  static_assert(PTW <= kXBlocks / kNW, "S_in stores precede the last copy part");
   __shared__ __attribute__((aligned(1024))) T xr[2][kQ * kP];
   __shared__ __attribute__((aligned(16))) float ar[2][kQ];
   __shared__ __attribute__((aligned(16))) float dr[HAS_DT ? 2 : 1][HAS_DT ? kQ : 4];
@@ -444,10 +445,6 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
 #pragma unroll
     for (int ks = 0; ks < kKS; ++ks) {
       set_prio(3 - ks / 2);
-      if (ks < PTW) {
-        if (!local) store_sin(c, ks);
-        else if (c > c0) store_local(c - 1, ks);  // st holds chunk c - 1's local state
-      }
       if (ks < kXBlocks / kNW && has_next) issue_copy_part(c + 1, bn, ks);
       const f32x4 w0 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 4 * g);
       const f32x4 w1 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 16 + 4 * g);
@@ -468,20 +465,26 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    // the chunk's stores go out after every load of the step; the wait
+    // leaves only them in flight (the next chunk's copies and B^T fragments
+    // have landed)
+    if (local) {
 #pragma unroll
-    for (int q = 0; q < PTW; ++q) st[q] = local ? acc[q] : st[q] * dec + acc[q];
-    // the next chunk's copies were issued before the B^T loads of K steps
-    // 4..7 (the only vector memory operations after them): they have landed
-    // once at most those 4 are outstanding
-    vm_wait<kKS - kXBlocks / kNW>();
+      for (int q = 0; q < PTW; ++q) st[q] = acc[q];
+#pragma unroll
+      for (int q = 0; q < PTW; ++q) store_local(c, q);
+    } else {
+#pragma unroll
+      for (int q = 0; q < PTW; ++q) store_sin(c, q);
+#pragma unroll
+      for (int q = 0; q < PTW; ++q) st[q] = st[q] * dec + acc[q];
+    }
+    vm_wait<PTW>();
     __syncthreads();
     if (has_next) tabulate(bn);
     __syncthreads();
   }
-  if (local) {
-#pragma unroll
-    for (int q = 0; q < PTW; ++q) store_local(c1 - 1, q);
-  } else if (sp.final_state) {
+  if (!local && sp.final_state) {
 #pragma unroll
     for (int q = 0; q < PTW; ++q)
       *reinterpret_cast<f32x4*>(sp.final_state + (int64_t)bh * (kP * N) + srow + 16 * N * q) = st[q];
