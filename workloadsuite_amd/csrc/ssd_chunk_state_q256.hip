@@ -184,12 +184,7 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
       const f32x4 w0 = *reinterpret_cast<const f32x4*>(wh + 32 * ks + 4 * g);
       const f32x4 w1 = *reinterpret_cast<const f32x4*>(wh + 32 * ks + 16 + 4 * g);
       frag8<T> hi, lo;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float v = to_f32<T>(bt[ks][j]) * (j < 4 ? w0[j] : w1[j - 4]);
-        hi[j] = from_f32<T>(v);
-        lo[j] = from_f32<T>(v - to_f32<T>(hi[j]));
-      }
+      split_weighted<T>(bt[ks], w0, w1, hi, lo);
 #pragma unroll
       for (int q = 0; q < PTW; ++q) {
         const T* a0 = xb + xoff[q] + (32 * ks) * kP;
@@ -449,12 +444,7 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
       const f32x4 w0 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 4 * g);
       const f32x4 w1 = *reinterpret_cast<const f32x4*>(wr + 32 * ks + 16 + 4 * g);
       frag8<T> hi, lo;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const float v = to_f32<T>(bt[ks][j]) * (j < 4 ? w0[j] : w1[j - 4]);
-        hi[j] = from_f32<T>(v);
-        lo[j] = from_f32<T>(v - to_f32<T>(hi[j]));
-      }
+      split_weighted<T>(bt[ks], w0, w1, hi, lo);
       bt[ks] = bnext[ks * 64];  // (the last chunk reloads its own: no branch, no register copies)
 #pragma unroll
       for (int q = 0; q < PTW; ++q) {

@@ -15,6 +15,8 @@
 // an A operand without an LDS round trip.
 #pragma once
 
+#include <type_traits>
+
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -61,6 +63,35 @@ __device__ __forceinline__ f32x4 mma(f32x8 a, f32x8 b, f32x4 c) {
 // ---------------------------------------------------------------------------
 template <typename T> __device__ __forceinline__ T from_f32(float v) { return (T)v; }
 template <typename T> __device__ __forceinline__ float to_f32(T v) { return (float)v; }
+
+// chunk_state's weighted B^T operand as a hi + lo pair of T: v = b w,
+// hi = T(v), lo = T(b w - float(hi)), the residual formed exactly by one
+// fma.  Pairs of elements take one packed conversion each way (for bf16 hi's
+// f32 value is read back from its bits): fewer instructions than converting
+// one value at a time, same values.
+template <typename T>
+__device__ __forceinline__ void split_weighted(const frag8<T>& b, f32x4 w0, f32x4 w1, frag8<T>& hi, frag8<T>& lo) {
+  typedef T t2 __attribute__((ext_vector_type(2)));
+  typedef float f32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    const float wa = j < 4 ? w0[j] : w1[j - 4], wb = j < 4 ? w0[j + 1] : w1[j - 3];
+    const float b0 = (float)b[j], b1 = (float)b[j + 1];
+    const t2 h = __builtin_convertvector((f32x2{b0 * wa, b1 * wb}), t2);
+    f32x2 hf;
+    if constexpr (std::is_same<T, bf16>::value) {
+      const uint32_t hu = __builtin_bit_cast(uint32_t, h);
+      hf = f32x2{__uint_as_float(hu << 16), __uint_as_float(hu & 0xffff0000u)};
+    } else {
+      hf = __builtin_convertvector(h, f32x2);
+    }
+    const t2 l = __builtin_convertvector((f32x2{__builtin_fmaf(b0, wa, -hf[0]), __builtin_fmaf(b1, wb, -hf[1])}), t2);
+    hi[j] = h[0];
+    hi[j + 1] = h[1];
+    lo[j] = l[0];
+    lo[j + 1] = l[1];
+  }
+}
 
 template <typename T> __device__ __forceinline__ frag8<T> zero_frag() {
   frag8<T> z;
