@@ -13,10 +13,12 @@
 //   btf  the B^T MFMA operands of chunk_state (MR:148 contracts over the
 //        chunk's tokens): n tile nt, 32-token step ks, lane (g, i) holds
 //        B[32 ks + slot_token(g, j)][16 nt + i] for j = 0..7.
-// One workgroup per (b, c, g): B and C of the chunk are copied to LDS (rows
+// One workgroup per (b, c, g): B of the chunk is copied to LDS (rows
 // XOR-swizzled by 16-byte piece so the 16 rows of an operand read hit
-// distinct banks), then each wave forms its CB^T blocks with the same MFMA
+// distinct banks) and each wave loads the C rows of its two row tiles into
+// registers; each wave then forms its CB^T blocks with the same MFMA
 // sequence as chunk_scan's own fallback, so both give bit-identical values.
+// 64 KB of LDS (N = 128) lets two workgroups share a CU.
 //
 // The forward launches K0 and K1 (ssd_cumsum_body.h) together: the first
 // workgroups of the grid do K0, the rest two K1 blocks each (one per 256
@@ -39,7 +41,7 @@ constexpr int kNW = 8;
 constexpr int kThreads = 64 * kNW;
 constexpr int kNPair = kQ / 32 + 1;  // CB^T steps per wave (two row tiles)
 
-template <int NK> constexpr int prep_lds_bytes() { return 2 * kQ * (64 * NK); }  // B and C rows
+template <int NK> constexpr int prep_lds_bytes() { return kQ * (64 * NK); }  // B rows
 
 // K0 for group bcg = (b * nchunks + c) * ngroups + grp, on lds (prep_lds_bytes, 1 KB aligned).
 template <typename T, int NK>
@@ -50,7 +52,6 @@ __device__ __forceinline__ void prep_body(const ChunkPrepArgs& p, int bcg, unsig
   constexpr int RPD = 1024 / RB; // rows per 64-lane copy
   constexpr int NTILE = N / 16;
   unsigned char* bl = lds;
-  unsigned char* cl = lds + kQ * RB;
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int g = lane >> 4, i = lane & 15;
@@ -58,16 +59,23 @@ __device__ __forceinline__ void prep_body(const ChunkPrepArgs& p, int bcg, unsig
   const int c = bc % p.nchunks, b = bc / p.nchunks;
   auto sw = [](int r) __attribute__((always_inline)) { return PPR >= 16 ? (r & 15) : ((r >> 1) & 7); };
 
-  // ---- B and C of the chunk -> LDS: copy d moves rows RPD d .. RPD d + RPD - 1 ----
+  // ---- B of the chunk -> LDS (copy d moves rows RPD d .. RPD d + RPD - 1);
+  // this wave's C rows straight into registers ----
   const int64_t l0 = (int64_t)c * kQ;
   const T* bg = reinterpret_cast<const T*>(p.bm) + (int64_t)b * p.sbb + l0 * p.sbl + (int64_t)grp * p.sbg;
   const T* cg = reinterpret_cast<const T*>(p.cm) + (int64_t)b * p.scb + l0 * p.scl + (int64_t)grp * p.scg;
-  const uint32_t bl_lds = lds_offset(bl), cl_lds = lds_offset(cl);
+  const uint32_t bl_lds = lds_offset(bl);
   for (int d = wave; d < kQ / RPD; d += kNW) {
     const int r = d * RPD + lane / PPR;
     const int piece = (lane % PPR) ^ sw(r);
     dma16_at(bg + (int64_t)r * p.sbl + 8 * piece, bl_lds + (uint32_t)(d * 1024));
-    dma16_at(cg + (int64_t)r * p.scl + 8 * piece, cl_lds + (uint32_t)(d * 1024));
+  }
+  const int ta = wave, tb = 15 - wave, KA = ta / 2 + 1;
+  frag8<T> cf[2][NK];
+#pragma unroll
+  for (int kc = 0; kc < NK; ++kc) {
+    cf[0][kc] = load8<T>(cg + (int64_t)(16 * ta + i) * p.scl + 8 * (4 * kc + g));
+    cf[1][kc] = load8<T>(cg + (int64_t)(16 * tb + i) * p.scl + 8 * (4 * kc + g));
   }
   dma_wait();
   __syncthreads();
@@ -78,13 +86,6 @@ __device__ __forceinline__ void prep_body(const ChunkPrepArgs& p, int bcg, unsig
   };
 
   // ---- CB^T blocks of wave w's row tiles ta = w and tb = 15 - w ----
-  const int ta = wave, tb = 15 - wave, KA = ta / 2 + 1;
-  frag8<T> cf[2][NK];
-#pragma unroll
-  for (int kc = 0; kc < NK; ++kc) {
-    cf[0][kc] = rd(cl, 16 * ta + i, 4 * kc + g);
-    cf[1][kc] = rd(cl, 16 * tb + i, 4 * kc + g);
-  }
   f32x4* out = reinterpret_cast<f32x4*>(p.cbf) + (int64_t)(bcg * kNW + wave) * kNPair * 2 * 64 + lane;
 #pragma unroll
   for (int k = 0; k < kNPair; ++k) {
@@ -129,10 +130,14 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkPrepArgs p) {
 }
 
 // K0 for the first nprep workgroups, then two K1 blocks (chunk 256) per workgroup.
+// K0's B rows or two K1 tiles
+template <int NK> constexpr int prologue_lds_bytes() {
+  return prep_lds_bytes<NK>() > (int)(2 * sizeof(CumsumTile<kQ>)) ? prep_lds_bytes<NK>() : (int)(2 * sizeof(CumsumTile<kQ>));
+}
+
 template <typename T, int NK, typename R, bool RAW>
 __global__ __launch_bounds__(kThreads) void chunk_prologue_kernel(ChunkPrepArgs p, CumsumArgs ca, int nprep) {
-  __shared__ __attribute__((aligned(1024))) unsigned char lds[prep_lds_bytes<NK>()];
-  static_assert(2 * sizeof(CumsumTile<kQ>) <= prep_lds_bytes<NK>(), "K1 tiles fit in K0's LDS");
+  __shared__ __attribute__((aligned(1024))) unsigned char lds[prologue_lds_bytes<NK>()];
   if ((int)blockIdx.x < nprep) {
     prep_body<T, NK>(p, blockIdx.x, lds);
     return;
