@@ -21,8 +21,8 @@
 // 64 KB of LDS (N = 128) lets two workgroups share a CU.
 //
 // The forward launches K0 and K1 (ssd_cumsum_body.h) together: the first
-// workgroups of the grid do K0, the rest two K1 blocks each (one per 256
-// threads) on the same LDS.  Both are short and independent; together they
+// workgroups of the grid do two K1 blocks each (one per 256 threads), the
+// rest K0, on the same LDS.  Both are short and independent; together they
 // fill the GPU that K0's few workgroups alone leave mostly idle, and one
 // kernel boundary goes away.
 #include <cstdint>
@@ -129,21 +129,23 @@ __global__ __launch_bounds__(kThreads) void chunk_prep_kernel(ChunkPrepArgs p) {
   prep_body<T, NK>(p, blockIdx.x, lds);
 }
 
-// K0 for the first nprep workgroups, then two K1 blocks (chunk 256) per workgroup.
 // K0's B rows or two K1 tiles
 template <int NK> constexpr int prologue_lds_bytes() {
   return prep_lds_bytes<NK>() > (int)(2 * sizeof(CumsumTile<kQ>)) ? prep_lds_bytes<NK>() : (int)(2 * sizeof(CumsumTile<kQ>));
 }
 
+// Two K1 blocks (chunk 256) per workgroup for the first nk1 workgroups, then
+// K0.  K1's short, latency-bound blocks are dispatched first, so that they
+// run beside K0's workgroups instead of after them when K0 fills the GPU.
 template <typename T, int NK, typename R, bool RAW>
-__global__ __launch_bounds__(kThreads) void chunk_prologue_kernel(ChunkPrepArgs p, CumsumArgs ca, int nprep) {
+__global__ __launch_bounds__(kThreads) void chunk_prologue_kernel(ChunkPrepArgs p, CumsumArgs ca, int nk1) {
   __shared__ __attribute__((aligned(1024))) unsigned char lds[prologue_lds_bytes<NK>()];
-  if ((int)blockIdx.x < nprep) {
-    prep_body<T, NK>(p, blockIdx.x, lds);
+  if ((int)blockIdx.x >= nk1) {
+    prep_body<T, NK>(p, (int)blockIdx.x - nk1, lds);
     return;
   }
   const int half = threadIdx.x >> 8, t = threadIdx.x & 255;
-  const int blk = 2 * ((int)blockIdx.x - nprep) + half;
+  const int blk = 2 * (int)blockIdx.x + half;
   CumsumTile<kQ>& tile = *reinterpret_cast<CumsumTile<kQ>*>(lds + half * sizeof(CumsumTile<kQ>));
   const bool valid = blk < cumsum_blocks(ca);
   if (valid) cumsum_load<kQ, R, RAW>(ca, blk, t, tile);
@@ -165,10 +167,11 @@ hipError_t launch_t(const ChunkPrepArgs& a, hipStream_t stream) {
 template <typename T, typename R, bool RAW>
 hipError_t launch_prologue_t(const ChunkPrepArgs& a, const CumsumArgs& ca, hipStream_t stream) {
   const int nprep = a.batch * a.nchunks * a.ngroups;
-  const unsigned grid = (unsigned)(nprep + (cumsum_blocks(ca) + 1) / 2);
+  const int nk1 = (cumsum_blocks(ca) + 1) / 2;
+  const unsigned grid = (unsigned)(nprep + nk1);
   switch (a.dstate) {
-    case 64: chunk_prologue_kernel<T, 2, R, RAW><<<grid, kThreads, 0, stream>>>(a, ca, nprep); break;
-    case 128: chunk_prologue_kernel<T, 4, R, RAW><<<grid, kThreads, 0, stream>>>(a, ca, nprep); break;
+    case 64: chunk_prologue_kernel<T, 2, R, RAW><<<grid, kThreads, 0, stream>>>(a, ca, nk1); break;
+    case 128: chunk_prologue_kernel<T, 4, R, RAW><<<grid, kThreads, 0, stream>>>(a, ca, nk1); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
