@@ -182,13 +182,13 @@ def test_chunk_scan_epilogue_rejects_mismatched_gate():
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("N,g", [(128, 2), (64, 4)])
-def test_ssd_layer_equals_its_kernels_one_by_one(dtype, N, g):
+@pytest.mark.parametrize("N,g,h", [(128, 2, 8), (64, 4, 8), (128, 4, 64)])
+def test_ssd_layer_equals_its_kernels_one_by_one(dtype, N, g, h):
     """ssd_layer (conv, then K1's layer variant inside K0's launch, K0 writing
     CB^T in the input type for K4's epilogue variant) against the public
     entry points called one by one: bit-identical."""
-    say("ssd_layer == kernels", dtype, N, g)
-    h, P, Q, L, b = 8, 64, 256, 512, 2
+    say("ssd_layer == kernels", dtype, N, g, h)
+    P, Q, L, b = 64, 256, 512, 2
     proj, prm = layer_case(dtype, b=b, L=L, h=h, P=P, g=g, N=N)
     pd = proj.to(DEV)
     x, z, B, C, dt = split(pd, h, P, g, N)
