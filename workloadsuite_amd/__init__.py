@@ -8,6 +8,7 @@ Kernels live in ``libssd.so`` (built by ``python -m workloadsuite_amd.build``);
 the C ABI is ``include/ssd.h``.
 """
 
+from . import torch_ops  # noqa: F401,E402  (torch.ops.workloadsuite_amd.ssd_forward / ssd_layer)
 from .ssd import (SSDError, chunk_cumsum, chunk_prep, chunk_scan, chunk_state, chunk_state_passing, decode_step,
                   layer_prep, ssd_core, ssd_forward, ssd_layer, state_passing, workspace_bytes)
 

@@ -30,7 +30,7 @@ from __future__ import annotations
 import torch
 import torch.nn as nn
 
-from .ssd import ssd_layer
+from . import torch_ops  # noqa: F401  (registers torch.ops.workloadsuite_amd.*)
 
 __all__ = ["SSDLayer", "Model", "get_inputs", "get_init_inputs"]
 
@@ -69,8 +69,10 @@ class SSDLayer(nn.Module):
         h, g, N = self.n_heads, self.n_groups, self.d_state
         zxbcdt = self.in_proj(self.norm(u))
         x, z, B, C, dt = torch.split(zxbcdt, [self.d_inner, self.d_inner, g * N, g * N, h], dim=-1)
-        Y = ssd_layer(x, z, B.view(b, L, g, N), C.view(b, L, g, N), dt, self.conv1d.weight, self.conv1d.bias,
-                      self.dt_bias, self.A_log, self.D, self.block_len, h)
+        # the registered op (one node for torch.compile) around ssd.ssd_layer
+        Y = torch.ops.workloadsuite_amd.ssd_layer(x, z, B.view(b, L, g, N), C.view(b, L, g, N), dt,
+                                                  self.conv1d.weight, self.conv1d.bias, self.dt_bias, self.A_log,
+                                                  self.D, self.block_len, h)
         return self.out_proj(Y)
 
 

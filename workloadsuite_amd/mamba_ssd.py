@@ -23,7 +23,7 @@ import torch
 import torch.nn as nn
 
 from .configs import CONFIGS, SSDConfig, make_inputs
-from .ssd import ssd_forward
+from . import torch_ops  # noqa: F401  (registers torch.ops.workloadsuite_amd.*)
 
 __all__ = ["Model", "get_inputs", "get_init_inputs", "build_workload", "CONFIGS"]
 
@@ -54,8 +54,11 @@ class Model(nn.Module):
         self.C = nn.Parameter(torch.randn(batch_size, seq_length, g, d_state).to(dtype))
 
     def forward(self, X: torch.Tensor, initial_states: torch.Tensor | None = None):
-        return ssd_forward(X, self.A, self.B, self.C, self.block_len, initial_states=initial_states,
-                           return_final_states=self.return_final_state, state_dtype=self.state_dtype)
+        # the registered op, so that torch.compile traces it as one node
+        Y, final = torch.ops.workloadsuite_amd.ssd_forward(X, self.A, self.B, self.C, self.block_len, None,
+                                                           initial_states, self.return_final_state,
+                                                           self.state_dtype)
+        return (Y, final) if self.return_final_state else Y
 
 
 # ----- module-level defaults: configuration C1 -----
