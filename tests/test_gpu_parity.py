@@ -271,6 +271,37 @@ def test_config_full_size(name, batches, heads):
     assert_close(fg, fr, tol, atol=fatol)
 
 
+@pytest.mark.parametrize("name", ["C3", "C4"])
+def test_full_size_chunk_invariance_and_state_linearity(name):
+    """Size-independent properties of the whole forward at the full config
+    size (the oracle is too slow there): the chunked SSD computes one linear
+    recurrence whatever the chunk length (MR:152-161), so the chunk-256
+    persistent path (state chain, chunk_scan's persistent kernel) and the
+    chunk-64 generic kernels agree; and Y is linear in the initial state,
+    Y(X, S0) = Y(X, 0) + Y(0, S0), as is the final state.  Tolerances are the
+    16-bit one relative to each output's scale (every Y is rounded to bf16
+    once)."""
+    cfg = CONFIGS[name]
+    say("full-size properties", name)
+    inp = to_dev(make_inputs(cfg, seed=3, device=DEV))
+    X, A, B, C = inp["X"], inp["A"], inp["B"], inp["C"]
+    gen = torch.Generator(device=DEV).manual_seed(4)
+    S0 = 0.1 * torch.randn(cfg.batch, cfg.nheads, cfg.headdim, cfg.dstate, device=DEV, generator=gen)
+    Y256, f256 = S.ssd_forward(X, A, B, C, 256, return_final_states=True)
+    Y64, f64 = S.ssd_forward(X, A, B, C, 64, return_final_states=True)
+    Yi, fi = S.ssd_forward(X, A, B, C, 256, initial_states=S0, return_final_states=True)
+    Y0, f0 = S.ssd_forward(torch.zeros_like(X), A, B, C, 256, initial_states=S0, return_final_states=True)
+    torch.cuda.synchronize()
+    tol = tolerance(cfg.dtype)
+    scale = Y256.float().abs().max().item()
+    fscale = f256.abs().max().item()
+    assert torch.isfinite(Y256).all() and torch.isfinite(f256).all()
+    assert_close(Y64, Y256.float(), tol, atol=tol * scale)
+    assert_close(f64, f256, tol, atol=tol * fscale)
+    assert_close(Yi, Y256.float() + Y0.float(), tol, atol=tol * scale)
+    assert_close(fi, f256 + f0, tol, atol=tol * fscale)
+
+
 def test_long_context_weak_decay_recurrence():
     """C4 shape with A scaled by 1e-3: 256 chunks of carried state dominate."""
     cfg = CONFIGS["C4"]
