@@ -403,3 +403,47 @@ def test_ssd_core_takes_the_reference_arguments():
     assert Y.shape == (b, c, l, h, p) and Y.dtype == torch.float16
     Ys, _ = O.ssd_sequential(x, A_dt, Bg, Cg, dt=dt)
     assert_close(Y.reshape(b, c * l, h, p), Ys, 2e-2)
+
+
+# ---------------------------------------------------------------------------
+# seeded random shapes: every launch plan against the oracle
+# ---------------------------------------------------------------------------
+
+def _random_cases(n, seed=11):
+    rng = np.random.default_rng(seed)
+    cases = []
+    for k in range(n):
+        dtype = [torch.float32, torch.bfloat16, torch.float16][k % 3]
+        Q = int(rng.choice([64, 128, 256]))
+        N = int(rng.choice([16, 32, 64, 128]))
+        g = int(rng.choice([1, 2, 4]))
+        h = g * int(rng.integers(1, 6))
+        if k % 5 == 4 and dtype != torch.float32:
+            Q, N, h = 256, 128, 160   # 2 x 160 = 320 chains: the state chain's mixed plan at 256 CUs
+        b = int(rng.integers(1, 3))
+        nc = int(rng.integers(1, 4))
+        cases.append((k, dtype, Q, N, g, h, b, nc, bool(rng.integers(0, 2)), bool(rng.integers(0, 2))))
+    return cases
+
+
+@pytest.mark.parametrize("k,dtype,Q,N,g,h,b,nc,use_dt,use_init", _random_cases(20))
+def test_random_shapes_vs_oracle(k, dtype, Q, N, g, h, b, nc, use_dt, use_init):
+    """Seeded random shapes (dtype, chunk, d_state, groups, heads, batch,
+    chunks, dt, initial state) through ssd_forward against the chunked
+    oracle, Y and the final state."""
+    say("random", k, dtype, Q, N, g, h, b, nc, use_dt, use_init)
+    cfg = CONFIGS["C2"].scaled(batch=b, seqlen=Q * nc, nheads=h, dstate=N, chunk=Q, ngroups=g, dtype=dtype,
+                               init_state=use_init)
+    inp = make_inputs(cfg, seed=100 + k)
+    gen = torch.Generator().manual_seed(200 + k)
+    dt = (torch.rand(b, Q * nc, h, generator=gen) + 0.1) if use_dt else None
+    d = to_dev(inp)
+    Y, final = S.ssd_forward(d["X"], d["A"], d["B"], d["C"], Q, dt=None if dt is None else dt.to(DEV),
+                             initial_states=d["init"], return_final_states=True)
+    torch.cuda.synchronize()
+    Yr, fr = O.ssd_chunked(inp["X"], inp["A"], inp["B"], inp["C"], Q, dt=dt, initial_states=inp["init"])
+    tol = tolerance(dtype)
+    atol = tol if dtype != torch.float32 else 1e-4 * max(Yr.abs().max().item(), 1.0)
+    assert_close(Y, Yr, tol, atol=atol)
+    fatol = tol if dtype != torch.float32 else 1e-4 * max(fr.abs().max().item(), 1.0)
+    assert_close(final, fr, tol, atol=fatol)
