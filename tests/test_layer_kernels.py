@@ -201,3 +201,33 @@ def test_ssd_layer_equals_its_kernels_one_by_one(dtype, N, g, h):
     yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dto, prep=prep, split=True, D=dev["D"], z=z.reshape(b, L, h, P))
     torch.cuda.synchronize()
     assert torch.equal(y, yk.reshape(b, L, h * P))
+
+
+def _random_layer_cases(n, seed=23):
+    """Seeded shapes for the fused span: dtype, chunk, state size, groups,
+    heads per group, batch, chunks, conv width and a column offset of the
+    slices inside in_proj's output."""
+    gen = torch.Generator().manual_seed(seed)
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=gen))]  # noqa: E731
+    cases = []
+    for k in range(n):
+        dtype = DTYPES[k % 3]
+        Q, N, g = pick([64, 128, 256]), pick([32, 64, 128]), pick([1, 2, 4])
+        h = g * pick([1, 2, 3])
+        b, nc = pick([1, 2]), pick([1, 2, 3])
+        cases.append((k, dtype, Q, N, g, h, b, Q * nc, pick([2, 3, 4]), pick([0, 8])))
+    return cases
+
+
+@pytest.mark.parametrize("k,dtype,Q,N,g,h,b,L,kw,pad", _random_layer_cases(12))
+def test_random_layer_shapes_vs_oracle(k, dtype, Q, N, g, h, b, L, kw, pad):
+    say("random ssd_layer", k, dtype, Q, N, g, h, b, L, kw, pad)
+    P = 64
+    proj, prm = layer_case(dtype, b=b, L=L, h=h, P=P, g=g, N=N, k=kw, pad=pad, seed=200 + k)
+    x, z, B, C, dt = split(proj, h, P, g, N, pad)
+    xd, zd, Bd, Cd, dtd = split(proj.to(DEV), h, P, g, N, pad)
+    y = S.ssd_layer(xd, zd, Bd, Cd, dtd, prm["conv_w"].to(DEV), prm["conv_b"].to(DEV), prm["dt_bias"].to(DEV),
+                    prm["A_log"].to(DEV), prm["D"].to(DEV), Q, h)
+    rX, rdt, rA, _, _ = ref_prep(x, dt, prm, Q, h, P)
+    ref = gated_ref(rX, rA, B, C, rdt, Q, prm["D"], z.reshape(b, L, h, P)).reshape(b, L, h * P)
+    close(y, ref, tolerance(dtype))
