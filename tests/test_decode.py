@@ -109,3 +109,33 @@ def test_decode_rejects_bad_arguments_on_the_host():
     with pytest.raises(ValueError, match="float32"):
         S.decode_step(torch.zeros(1, 2, 64, 16, dtype=torch.float16), torch.zeros(1, 2, 64), torch.zeros(1, 1, 16),
                       torch.zeros(1, 1, 16), torch.zeros(1, 2))
+
+
+def _random_decode_cases(n, seed=31):
+    gen = torch.Generator().manual_seed(seed)
+    pick = lambda seq: seq[int(torch.randint(len(seq), (1,), generator=gen))]  # noqa: E731
+    cases = []
+    for k in range(n):
+        g = pick([1, 2, 4])
+        cases.append((k, DTYPES[k % 3], pick([64, 128, 256]), pick([16, 64, 128]), g, g * pick([1, 2, 3]), pick([1, 3])))
+    return cases
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("k,dtype,Q,N,g,h,b", _random_decode_cases(9))
+def test_decode_several_steps_after_forward(k, dtype, Q, N, g, h, b):
+    """ssd_forward over one chunk, then four decode steps in a row on the
+    returned state: every step's y and the last state equal the sequential
+    recurrence over the whole sequence."""
+    say("decode steps after forward", k, dtype, Q, N, g, h, b)
+    steps = 4
+    X, A, B, C, dt = inputs(dtype, b, Q + steps, h, g, N, seed=300 + k)
+    Ys, fs = O.ssd_sequential(X, A, B, C, dt=dt)
+    d = lambda t: t.to(DEV)  # noqa: E731
+    _, state = S.ssd_forward(d(X[:, :Q]), d(A[:, :Q]), d(B[:, :Q]), d(C[:, :Q]), Q, dt=d(dt[:, :Q]),
+                             return_final_states=True)
+    for s in range(Q, Q + steps):
+        y = S.decode_step(state, d(X[:, s]), d(B[:, s]), d(C[:, s]), d(A[:, s]), dt=d(dt[:, s]))
+        close(y, Ys[:, s], tolerance(dtype))
+    scale = float(np.abs(fs).max())
+    close(state / scale, fs / scale, 1e-4)
