@@ -104,15 +104,43 @@ def end_to_end_model(cfg):
 
 def profiled_traffic(cfg, kernel):
     """HBM bytes per launch of `kernel` as measured with rocprofv3 FETCH_SIZE /
-    WRITE_SIZE (scaled by a copy of known size) and committed under profiles/;
-    (None, None) when there is no such measurement for this workload."""
+    WRITE_SIZE (scaled by a copy of known size) and committed under
+    profiles/ssd_forward_<config>.md as a line ``traffic_bytes_per_launch
+    <kernel>: <bytes>``; (None, None) when there is no such measurement."""
     path = os.path.join(ROOT, "profiles", f"ssd_forward_{cfg.name}.md")
-    if kernel != "chunk_scan" or not os.path.exists(path):
+    if not os.path.exists(path):
         return None, None
+    key = f"traffic_bytes_per_launch {kernel}:"
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
-            return int(line.split(":")[1]), os.path.relpath(path, ROOT)
+        if line.startswith(key):
+            return int(line[len(key):].strip()), os.path.relpath(path, ROOT)
     return None, None
+
+
+def summarize(samples):
+    """median / mean / p90 / p99 of per-step times (ms), quantiles by nearest
+    rank on the sorted samples, index round(q (n - 1)) (the reference
+    harness's convention, bench.py:123-135 of ShouyangDong/WorkloadSuite)."""
+    srt = sorted(samples)
+
+    def q(x):
+        return srt[min(len(srt) - 1, max(0, round(x * (len(srt) - 1))))]
+
+    return {"median_ms": round(statistics.median(srt), 5), "mean_ms": round(statistics.mean(srt), 5),
+            "p90_ms": round(q(0.90), 5), "p99_ms": round(q(0.99), 5), "runs": len(srt)}
+
+
+def step_stats(fn, runs):
+    """Per-call device time of fn(): an event pair around each of `runs`
+    back-to-back calls on the current stream."""
+    torch.cuda.synchronize()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(runs)]
+    for a, b in ev:
+        a.record()
+        fn()
+        b.record()
+    torch.cuda.synchronize()
+    return summarize([a.elapsed_time(b) for a, b in ev])
 
 
 def time_launches(fn, reps):
@@ -287,6 +315,8 @@ def main():
     dev_ms = ev0.elapsed_time(ev1) / args.steps
     ms_per_step = wall * 1e3 / args.steps
     tokens_per_s = cfg.tokens * args.steps / wall
+    # the same K steps timed one by one (after the timed region above)
+    stats = step_stats(step, args.steps)
 
     # ---- per-kernel device time, each kernel on its real inputs ----
     Acs, decay = S.chunk_cumsum(A, cfg.chunk)
@@ -296,16 +326,27 @@ def main():
     # hands S_in to K4 as 16-bit (hi, lo) pairs
     split = cfg.dtype if (prep is not None and state_dtype == torch.float32) else None
     S_in, _ = S.state_passing(states, decay, init, split=split)
-    # K3 is timed in place on its own buffer, re-applying the recurrence to its
-    # own output on every launch: the same traffic and instructions (nothing in
-    # the kernel depends on the values, which stop being meaningful).
-    sp_buf = states.clone()
+    # K3 is timed in place on its own buffers, re-applying the recurrence to
+    # their contents on every launch: the same traffic and instructions (nothing
+    # in the kernel depends on the values, which stop being meaningful).  The
+    # launches rotate over enough buffers (at least two, at least 512 MB in
+    # all: twice the MI355X's 256 MB Infinity Cache) that each launch reads
+    # states that are no longer cached.
+    nbuf = max(2, -(-512 * 2**20 // states.numel() // states.element_size()))
+    sp_bufs = [states.clone() for _ in range(nbuf)]
+    sp_next = [0]
+
+    def sp_launch():
+        buf = sp_bufs[sp_next[0] % nbuf]
+        sp_next[0] += 1
+        return S.state_passing_(buf, decay, init, sp_final, split=split)
+
     sp_final = torch.empty(cfg.batch, cfg.nheads, cfg.headdim, cfg.dstate, device=dev) if cfg.final_state else None
     kfn = {
         "chunk_cumsum": lambda: S.chunk_cumsum(A, cfg.chunk),
         "chunk_prep": lambda: S.chunk_prep(B, C, cfg.chunk),
         "chunk_state": lambda: S.chunk_state(X, B, Acs, state_dtype=state_dtype, prep=prep),
-        "state_passing": lambda: S.state_passing_(sp_buf, decay, init, sp_final, split=split),
+        "state_passing": sp_launch,
         "chunk_state_passing": lambda: S.chunk_state_passing(X, B, Acs, decay, prep=prep, initial_states=init,
                                                              return_final_states=cfg.final_state, split=split,
                                                              state_dtype=state_dtype),
@@ -362,6 +403,7 @@ def main():
                    "inputs": f"{DTYPE_NAMES[cfg.dtype]} X/B/C, f32 A", "state_storage": args.state_dtype,
                    "final_state": cfg.final_state, "initial_state": cfg.init_state},
         "device_ms_per_step": round(dev_ms, 5),
+        "step_stats": stats,
         "roofline": roof,
         "end_to_end": {"F_min_per_token": f_min / cfg.tokens, "B_min_per_token": b_min / cfg.tokens,
                        "roofline_tokens_per_s": roof_tps, "frac": round(tokens_per_s / roof_tps, 4)},

@@ -1,7 +1,7 @@
 """Full-layer drop-in (workloads/mamba/model_ref.py, MR:13-121, 165-229).
 
-CPU: the layer oracle's steps are pinned against torch's own float64 library
-routines, and the HIP module's surface (constructor signatures, parameter
+CPU: the layer oracle's steps (and the model's residual stack) are pinned
+against torch's own float64 library routines, and the HIP module's surface (constructor signatures, parameter
 names, shapes and dtypes, module-level config) is checked against MR's as read
 from the reference source.  GPU (marked ``gpu``): the module on the MI355X
 against the float64 layer oracle with the same weights, rtol = atol = 2e-2
@@ -19,6 +19,7 @@ import torch.nn.functional as F
 from oracle import layer_oracle as LO
 from oracle import ssd_oracle as O
 from workloadsuite_amd import mamba_layer as ML
+from workloadsuite_amd import ssd as S
 
 DEV = "cuda"
 
@@ -86,6 +87,40 @@ def test_oracle_layer_equals_library_composition_with_sequential_core():
     Y = torch.from_numpy(Ys) + X * p["D"].reshape(1, 1, -1, 1)
     ref = F.linear(Y.reshape(b, L, d_inner) * F.silu(z), p["out_proj.weight"])
     torch.testing.assert_close(y, ref, rtol=1e-10, atol=1e-10)
+
+
+def test_oracle_model_equals_residual_composition():
+    """model_forward (MR:200-203) against its definition composed from torch's
+    own float64 F.rms_norm and the pinned layer_forward, two layers."""
+    g = torch.Generator().manual_seed(5)
+    h, P, N, G, Q, L, b, dm, k = 2, 8, 4, 1, 8, 16, 2, 12, 3
+    d_inner = h * P
+    d_proj = 2 * d_inner + 2 * G * N + h
+    r = lambda *s, sc=1.0: torch.randn(*s, generator=g, dtype=torch.float64) * sc  # noqa: E731
+
+    def params():
+        return {
+            "norm.weight": 1.0 + r(dm, sc=0.1),
+            "in_proj.weight": r(d_proj, dm, sc=dm ** -0.5),
+            "conv1d.weight": r(d_inner, 1, k, sc=0.5),
+            "conv1d.bias": r(d_inner, sc=0.1),
+            "A_log": r(h, sc=0.5),
+            "D": 1.0 + r(h, sc=0.1),
+            "dt_bias": r(h, sc=0.5) - 2.0,
+            "out_proj.weight": r(dm, d_inner, sc=d_inner ** -0.5),
+        }
+
+    layers = [params(), params()]
+    wf = 1.0 + r(dm, sc=0.1)
+    u = r(b, L, dm)
+    y = LO.model_forward(u, layers, wf, h, N, P, G, Q)
+    x = u
+    for p in layers:
+        x = x + LO.layer_forward(x, p, h, N, P, G, Q)
+    ref = F.rms_norm(x, (dm,), wf, eps=float(np.finfo(np.float16).eps))
+    torch.testing.assert_close(y, ref, rtol=1e-12, atol=1e-12)
+    # and the residual matters: one layer less gives another output
+    assert not torch.allclose(LO.model_forward(u, layers[:1], wf, h, N, P, G, Q), ref)
 
 
 # ---------------------------------------------------------------------------
@@ -163,14 +198,21 @@ def _randomize(model, seed):
     dict(d_model=256, n_layers=2, n_heads=8, d_state=64, d_head=64, n_groups=2, block_len=64, L=256, b=2),
     dict(d_model=256, n_layers=1, n_heads=8, d_state=128, d_head=64, n_groups=1, block_len=256, L=512, b=2),
     dict(d_model=2048, n_layers=1, n_heads=128, d_state=128, d_head=64, n_groups=8, block_len=64, L=128, b=1),
-], ids=["small-Q64", "small-Q256", "R0-widths"])
+    dict(d_model=512, n_layers=2, n_heads=16, d_state=128, d_head=64, n_groups=8, block_len=64, L=512, b=2,
+         mr_init=True),
+], ids=["small-Q64", "small-Q256", "R0-widths", "MR-init-chunk256"])
 def test_model_matches_layer_oracle(cfg):
+    """mr_init keeps the module's own initialisation (MR:58-66: default
+    nn.Linear / nn.Conv1d weights, A_log = log(1..h), dt_bias = -4, D = 1);
+    the other cases spread A and the gates wider.  L = 512 with block_len 64
+    runs the core at chunk 256, compared with the oracle at block_len 64."""
     say("layer", cfg)
     cfg = dict(cfg)
-    L, b = cfg.pop("L"), cfg.pop("b")
+    L, b, mr_init = cfg.pop("L"), cfg.pop("b"), cfg.pop("mr_init", False)
     torch.manual_seed(0)
     m = ML.Model(**cfg)
-    _randomize(m, seed=3)
+    if not mr_init:
+        _randomize(m, seed=3)
     m = m.to(DEV).eval()
     u = torch.randn(b, L, cfg["d_model"], generator=torch.Generator().manual_seed(4)).to(torch.float16)
     with torch.inference_mode():
@@ -183,14 +225,60 @@ def test_model_matches_layer_oracle(cfg):
     torch.testing.assert_close(y.double().cpu(), yr, rtol=2e-2, atol=2e-2)
 
 
+def _span_oracle(x, z, B, C, dt, layer, heads, block_len):
+    """float64 oracle of SSDLayer.forward between its projections (MR:83-118)
+    for some heads of one in_proj output: x, z [b, L, h*P], B, C [b, L, g, N],
+    dt [b, L, h] (CPU).  Heads are independent there, so each sampled head
+    runs the chunked oracle with its own group of B and C."""
+    P, h, g = layer.d_head, layer.n_heads, layer.n_groups
+    ch = torch.cat([torch.arange(hh * P, (hh + 1) * P) for hh in heads])
+    grp = torch.tensor([hh // (h // g) for hh in heads])
+    hs = torch.tensor(heads)
+    w = layer.conv1d.weight.detach().cpu().double()[ch]
+    bias = layer.conv1d.bias.detach().cpu().double()[ch]
+    X = LO.silu(LO.causal_depthwise_conv(x[..., ch].double(), w, bias))
+    b, L = x.shape[:2]
+    X = X.reshape(b, L, len(heads), P)
+    dtr = LO.softplus(dt[..., hs].double() + layer.dt_bias.detach().cpu().double()[hs])
+    A = -torch.exp(layer.A_log.detach().cpu().double()[hs]) * dtr
+    Y, _ = O.ssd_chunked(X, A, B[:, :, grp].double(), C[:, :, grp].double(), block_len, dt=dtr)
+    Y = Y + X * layer.D.detach().cpu().double()[hs].reshape(1, 1, -1, 1)
+    return Y.reshape(b, L, -1) * LO.silu(z[..., ch].double())
+
+
 @pytest.mark.gpu
-def test_full_r0_layer_runs_at_reference_size():
-    """MR's production shape, one layer (batch 8, seqlen 2048, d_model 2048)."""
-    say("R0 full size")
+def test_full_r0_layer_span_matches_oracle_with_reference_init():
+    """MR's production shape, one layer (batch 8, seqlen 2048, d_model 2048,
+    128 heads, d_state 128, 8 groups, block_len 64; MR:209-221) with the
+    module's own initialisation: A = -(1..128), dt = softplus(dt_raw - 4),
+    D = 1 (MR:61-63, 94), so in-chunk cumulative log-decays reach ~-600.  The
+    core runs at chunk 256 (1,024 chains: the whole-chain plan, and the
+    epilogue chunk_scan reading chunk_prep's 16-bit C.B^T).  The span's output
+    (out_proj's input) is compared on sampled batches and heads -- every group
+    is covered -- with the float64 oracle at MR's block_len 64, 2e-2."""
+    say("R0 full size, MR init")
     torch.manual_seed(0)
-    m = ML.Model(*[2048, 1, 128, 128, 64, 8, 64, 4]).to(DEV).eval()
-    u = torch.randn(ML.batch_size, ML.seq_length, 2048, device=DEV, dtype=torch.float16)
+    layer = ML.SSDLayer(2048, 128, 128, 64, 8, block_len=64, conv_kernel=4).to(DEV).eval()
+    u = torch.randn(ML.batch_size, ML.seq_length, 2048, device=DEV, dtype=torch.float16,
+                    generator=torch.Generator(device=DEV).manual_seed(1))
+    h, g, N, P = 128, 8, 128, 64
     with torch.inference_mode():
-        y = m(u)
+        zxbcdt = layer.in_proj(layer.norm(u))
+        x, z, B, C, dt = torch.split(zxbcdt, [h * P, h * P, g * N, g * N, h], dim=-1)
+        b, L = u.shape[:2]
+        Bv, Cv = B.view(b, L, g, N), C.view(b, L, g, N)
+        y = S.ssd_layer(x, z, Bv, Cv, dt, layer.conv1d.weight, layer.conv1d.bias, layer.dt_bias, layer.A_log,
+                        layer.D, 64, h)
+        y_mod = layer(u)
     torch.cuda.synchronize()
-    assert y.shape == u.shape and torch.isfinite(y).all()
+    assert y.shape == (b, L, h * P) and torch.isfinite(y).all() and torch.isfinite(y_mod).all()
+    heads = [0, 1, 17, 40, 63, 64, 100, 127]   # groups 0, 1, 2, 3, 4, 6, 7
+    bs = torch.tensor([0, 7])
+    cpu = lambda t: t[bs].cpu()  # noqa: E731
+    ref = _span_oracle(cpu(x), cpu(z), cpu(Bv), cpu(Cv), cpu(dt), layer, heads, 64)
+    ch = torch.cat([torch.arange(hh * P, (hh + 1) * P) for hh in heads])
+    got = y[bs].cpu()[..., ch]
+    torch.testing.assert_close(got.double(), ref, rtol=2e-2, atol=2e-2)
+    # the module's forward is that span followed by out_proj
+    with torch.inference_mode():
+        torch.testing.assert_close(y_mod, layer.out_proj(y), rtol=1e-3, atol=1e-3)

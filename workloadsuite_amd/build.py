@@ -37,7 +37,7 @@ SOURCES = [
 # Packed FP32 VALU forms are disabled: hipcc -O3 would otherwise emit
 # v_pk_{add,mul,fma}_f32 from plain float code.
 DEVICE_FLAGS = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-COMMON_FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-Wall", "-Wno-unused-function"]
+COMMON_FLAGS = ["-O3", "-fPIC", "-std=c++17", f"--offload-arch={ARCH}", "-Wall", "-Werror", "-Wno-unused-function"]
 
 
 def hipcc() -> str:

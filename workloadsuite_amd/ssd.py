@@ -139,6 +139,25 @@ def _dims(b, L, h, P, N, g, Q):
     return d
 
 
+def _expect(name, t, shape, dtype=None):
+    """Shape (and dtype) of a per-kernel operand the C ABI takes without sizes."""
+    if t is None:
+        return
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must be {tuple(shape)}, got {tuple(t.shape)}")
+    if dtype is not None and t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+def _check_prep(prep, d):
+    """chunk_prep's buffer must be at least what the dims need (it is read without a size)."""
+    if prep is None:
+        return
+    need = _lib.load().ssd_chunk_prep_bytes(ctypes.byref(d))
+    if need == 0 or prep.dtype != torch.uint8 or prep.numel() < need:
+        raise ValueError(f"prep must be chunk_prep(B, C, Q)'s buffer for these shapes ({need} bytes)")
+
+
 def workspace_bytes(batch, seqlen, nheads, headdim, dstate, ngroups, chunk_size,
                     state_dtype=torch.float32) -> int:
     d = _lib.dims(batch, seqlen, nheads, headdim, dstate, ngroups, chunk_size)
@@ -250,8 +269,13 @@ def chunk_state(X, B, Acs, dt=None, state_dtype=torch.float32, prep=None):
     b, L, h, P = X.shape
     g, N = B.shape[2], B.shape[3]
     Q = Acs.shape[-1]
-    dev = _device_check(X, B, Acs, dt)
+    dev = _device_check(X, B, Acs, dt, prep)
     d = _dims(b, L, h, P, N, g, Q)
+    _expect("Acs", Acs, (b, h, L // Q, Q))
+    _expect("dt", dt, (b, L, h))
+    _check_prep(prep, d)
+    if state_dtype not in _STATE_DTYPES:
+        raise ValueError(f"unsupported state dtype {state_dtype}")
     X, Bm = _vec_operand(X.detach()), _vec_operand(B.detach())
     Acs = _f32_contig(Acs)
     dt = _f32_operand(dt)
@@ -285,6 +309,10 @@ def state_passing_(states, chunk_decay, initial_states=None, final_states=None, 
     if not states.is_contiguous():
         raise ValueError("state_passing_ needs a contiguous states buffer")
     d = _dims(b, nc * 64, h, P, N, 1, 64)
+    if states.dtype not in _STATE_DTYPES:
+        raise ValueError(f"unsupported state dtype {states.dtype}")
+    _expect("chunk_decay", chunk_decay, (b, h, nc))
+    _expect("initial_states", initial_states, (b, h, P, N))
     decay = _f32_contig(chunk_decay)
     init = _f32_contig(initial_states)
     if final_states is not None and (final_states.dtype != torch.float32 or not final_states.is_contiguous()
@@ -307,8 +335,13 @@ def chunk_state_passing(X, B, Acs, chunk_decay, dt=None, prep=None, initial_stat
     b, L, h, P = X.shape
     g, N = B.shape[2], B.shape[3]
     Q = Acs.shape[-1]
-    dev = _device_check(X, B, Acs, chunk_decay, dt, initial_states)
+    dev = _device_check(X, B, Acs, chunk_decay, dt, initial_states, prep)
     d = _dims(b, L, h, P, N, g, Q)
+    _expect("Acs", Acs, (b, h, L // Q, Q))
+    _expect("chunk_decay", chunk_decay, (b, h, L // Q))
+    _expect("dt", dt, (b, L, h))
+    _expect("initial_states", initial_states, (b, h, P, N))
+    _check_prep(prep, d)
     X, Bm = _vec_operand(X.detach()), _vec_operand(B.detach())
     Acs = _f32_contig(Acs)
     decay = _f32_contig(chunk_decay)
@@ -363,8 +396,20 @@ def chunk_scan(X, B, C, Acs, states, dt=None, prep=None, split=False, D=None, z=
     b, L, h, P = X.shape
     g, N = B.shape[2], B.shape[3]
     Q = Acs.shape[-1]
-    dev = _device_check(X, B, C, Acs, states, dt)
+    dev = _device_check(X, B, C, Acs, states, dt, prep)
     d = _dims(b, L, h, P, N, g, Q)
+    if C.shape != B.shape or C.dtype != B.dtype:
+        raise ValueError("B and C must have the same shape and dtype")
+    _expect("Acs", Acs, (b, h, L // Q, Q))
+    _expect("dt", dt, (b, L, h))
+    # the kernels read [b, c, h, P, N] rows of the states' element size: a
+    # wrongly shaped or typed buffer would be read past its end
+    _expect("states", states, (b, L // Q, h, P, N), torch.float32 if split else None)
+    if not split and states.dtype not in _STATE_DTYPES:
+        raise ValueError(f"unsupported state dtype {states.dtype}")
+    if split and X.dtype not in _SPLIT_STATES:
+        raise ValueError("split states need 16-bit inputs")
+    _check_prep(prep, d)
     X, Bm, Cm = _vec_operand(X.detach()), _vec_operand(B.detach()), _vec_operand(C.detach())
     Acs = _f32_contig(Acs)
     dt = _f32_operand(dt)
@@ -400,7 +445,9 @@ def decode_step(state, x, B, C, a, dt=None, D=None, z=None):
         raise ValueError("x, B and C must share a supported dtype")
     if not state.is_contiguous() or state.data_ptr() % 16:
         raise ValueError("state must be contiguous and 16-byte aligned (it is updated in place)")
-    dev = _device_check(state, x, B, C, a, dt)
+    dev = _device_check(state, x, B, C, a, dt, D, z)
+    if D is not None and D.numel() != h:
+        raise ValueError(f"D must have {h} elements")
     d = _lib.dims(b, 1, h, P, N, g, 1)
     x, Bm, Cm = _rows3(x), _rows3(B), _rows3(C)
     a = _f32_contig(a)
