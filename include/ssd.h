@@ -283,6 +283,30 @@ int ssd_layer_forward(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
                       void* y, const int64_t y_strides[3],
                       void* workspace, size_t workspace_bytes, void* stream);
 
+/* ssd_forward without a workspace argument: the workspace is a device array
+ * of SSD_NOALLOC_SCRATCH_BYTES that the library keeps per device (from its
+ * first use on that device until the process ends), so the call itself
+ * allocates nothing.  No counterpart in the reference: it is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc).  Same arguments and results as
+ * ssd_forward otherwise; the caller still provides every input and output.
+ * When the workspace of the whole call (ssd_workspace_bytes) is larger than
+ * the array, the batch runs in slices whose workspace fits; a shape whose
+ * single batch element needs more returns SSD_ERR_WORKSPACE_TOO_SMALL before
+ * any launch.  All calls on one device share that device's array: calls that
+ * overlap on one device (other streams, other threads) race, so the caller
+ * serialises them. */
+#define SSD_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)
+int ssd_forward_noalloc(const ssd_dims* d, int dtype,
+                        const void* x, const int64_t x_strides[4],
+                        const float* a, const int64_t a_strides[3],
+                        const void* bmat, const int64_t b_strides[4],
+                        const void* cmat, const int64_t c_strides[4],
+                        const float* dt, const int64_t dt_strides[3],
+                        const float* initial_states,
+                        void* y, const int64_t y_strides[4],
+                        float* final_states, int state_dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,76 @@
+"""ssd_forward_noalloc (the entry point that allocates nothing: its workspace
+is a device array the library keeps per device) against ssd_forward with a
+caller-allocated workspace: the same kernels, so the same bits.  Two calls in
+a row, the second smaller; a call whose workspace exceeds the array (run in
+batch slices); an f32 call on the generic kernels; and a shape whose single
+batch element does not fit, rejected on the host before any launch."""
+
+import ctypes
+
+import pytest
+import torch
+
+from workloadsuite_amd import _lib
+from workloadsuite_amd import ssd as S
+from workloadsuite_amd.configs import CONFIGS, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda"
+SCRATCH = 256 << 20
+
+
+def run_both(cfg, seed, use_dt=False):
+    inp = make_inputs(cfg, seed=seed, device=DEV)
+    dt = (torch.rand(cfg.batch, cfg.seqlen, cfg.nheads, device=DEV) + 0.5) if use_dt else None
+    args = (inp["X"], inp["A"], inp["B"], inp["C"], cfg.chunk)
+    kw = dict(dt=dt, initial_states=inp["init"], return_final_states=True)
+    Y0, f0 = S.ssd_forward(*args, **kw)
+    Y1, f1 = S.ssd_forward_noalloc(*args, **kw)
+    torch.cuda.synchronize()
+    return Y0, f0, Y1, f1
+
+
+def test_noalloc_matches_forward_two_calls_second_smaller():
+    big = CONFIGS["C3"].scaled(batch=2)
+    small = CONFIGS["C3"].scaled(batch=1, seqlen=1024, nheads=16, init_state=True)
+    for cfg, seed, use_dt in ((big, 0, False), (small, 1, True)):
+        print("CASE noalloc", cfg, flush=True)
+        ws = S.workspace_bytes(cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, cfg.chunk)
+        assert ws <= SCRATCH
+        Y0, f0, Y1, f1 = run_both(cfg, seed, use_dt)
+        assert torch.equal(Y1, Y0) and torch.equal(f1, f0)
+
+
+def test_noalloc_runs_batch_slices_when_the_workspace_exceeds_the_array():
+    cfg = CONFIGS["C3"].scaled(batch=6, seqlen=4096)
+    ws = S.workspace_bytes(cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, cfg.chunk)
+    print("CASE noalloc slices", cfg, ws, flush=True)
+    assert ws > SCRATCH
+    Y0, f0, Y1, f1 = run_both(cfg, 2)
+    assert torch.equal(Y1, Y0) and torch.equal(f1, f0)
+
+
+def test_noalloc_f32_generic_kernels():
+    cfg = CONFIGS["C5"].scaled(batch=4)
+    print("CASE noalloc f32", cfg, flush=True)
+    Y0, f0, Y1, f1 = run_both(cfg, 3, use_dt=True)
+    assert torch.equal(Y1, Y0) and torch.equal(f1, f0)
+
+
+def test_noalloc_rejects_a_batch_element_larger_than_the_array():
+    cfg = CONFIGS["C4"]
+    one = S.workspace_bytes(1, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, cfg.chunk)
+    print("CASE noalloc too large", cfg, one, flush=True)
+    assert one > SCRATCH
+    inp = make_inputs(cfg, seed=0, device=DEV)
+    Y = torch.full_like(inp["X"], 7.0)
+    d = _lib.dims(cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, cfg.chunk)
+    p = lambda t: ctypes.c_void_p(t.data_ptr())  # noqa: E731
+    rc = _lib.load().ssd_forward_noalloc(
+        ctypes.byref(d), _lib.DTYPE_BF16, p(inp["X"]), _lib.strides(inp["X"]), p(inp["A"]), _lib.strides(inp["A"]),
+        p(inp["B"]), _lib.strides(inp["B"]), p(inp["C"]), _lib.strides(inp["C"]), None, None, None, p(Y),
+        _lib.strides(Y), None, _lib.DTYPE_F32, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+    torch.cuda.synchronize()
+    assert rc == -11  # SSD_ERR_WORKSPACE_TOO_SMALL
+    assert bool((Y == 7.0).all())  # nothing was launched

@@ -37,6 +37,7 @@ EXPORTS = (
     "ssd_layer_prep",
     "ssd_layer_workspace_bytes",
     "ssd_layer_forward",
+    "ssd_forward_noalloc",
 )
 
 
@@ -83,6 +84,8 @@ _SIGNATURES = {
     "ssd_layer_workspace_bytes": (ctypes.c_size_t, [_dims_p, _int]),
     "ssd_layer_forward": (_int, [_dims_p, _int, _prm_p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                                  _vp, _i64p, _vp, _i64p, _vp, ctypes.c_size_t, _vp]),
+    "ssd_forward_noalloc": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
+                                   _vp, _vp, _i64p, _vp, _int, _vp]),
 }
 
 _LIB = None

@@ -32,6 +32,7 @@ SOURCES = [
     "ssd_chunk_scan_q256.hip",
     "ssd_layer_prep.hip",
     "ssd_decode.hip",
+    "ssd_noalloc.hip",
 ]
 
 # Packed FP32 VALU forms are disabled: hipcc -O3 would otherwise emit

@@ -35,6 +35,7 @@ from . import _lib
 
 __all__ = [
     "ssd_forward",
+    "ssd_forward_noalloc",
     "ssd_core",
     "chunk_cumsum",
     "chunk_prep",
@@ -199,6 +200,39 @@ def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
                          _ptr(dt), _lib.strides(dt) if dt is not None else None,
                          _ptr(init), _ptr(Y), _lib.strides(Y), _ptr(final),
                          _ptr(ws), ws_n, sd, _stream(dev))
+    _lib.check(rc)
+    return (Y, final) if return_final_states else Y
+
+
+def ssd_forward_noalloc(X, A, B, C, chunk_size, dt=None, initial_states=None,
+                        return_final_states=False, state_dtype=torch.float32):
+    """``ssd_forward`` through the C ABI's ``ssd_forward_noalloc``: the library
+    takes its workspace from a device array it keeps per device instead of a
+    buffer allocated here (for callers that cannot allocate: graph capture,
+    serving loops).  Same results.  Only the outputs are allocated (by torch,
+    before the call); inputs that are not already in the kernels' layout are
+    copied first, as in ``ssd_forward``.  Calls that overlap on one device race
+    on that array."""
+    b, L, h, P, g, N = _shape_check(X, A, B, C, chunk_size, dt, initial_states)
+    dev = _device_check(X, A, B, C, dt, initial_states)
+    lib = _lib.load()
+    d = _dims(b, L, h, P, N, g, chunk_size)
+    sd = _STATE_DTYPES.get(state_dtype)
+    if sd is None:
+        raise ValueError(f"unsupported state dtype {state_dtype}")
+    X = _vec_operand(X.detach())
+    Bm = _vec_operand(B.detach())
+    Cm = _vec_operand(C.detach())
+    A = _f32_operand(A)
+    dt = _f32_operand(dt)
+    init = _f32_contig(initial_states)
+    Y = torch.empty((b, L, h, P), dtype=X.dtype, device=dev)
+    final = torch.empty((b, h, P, N), dtype=torch.float32, device=dev) if return_final_states else None
+    rc = lib.ssd_forward_noalloc(ctypes.byref(d), _DTYPES[X.dtype],
+                                 _ptr(X), _lib.strides(X), _ptr(A), _lib.strides(A),
+                                 _ptr(Bm), _lib.strides(Bm), _ptr(Cm), _lib.strides(Cm),
+                                 _ptr(dt), _lib.strides(dt) if dt is not None else None,
+                                 _ptr(init), _ptr(Y), _lib.strides(Y), _ptr(final), sd, _stream(dev))
     _lib.check(rc)
     return (Y, final) if return_final_states else Y
 
