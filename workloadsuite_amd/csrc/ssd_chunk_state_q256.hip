@@ -394,11 +394,14 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
   auto store_sin = [&](int c, int q) __attribute__((always_inline)) {
+    // from the f32 state (opaque: no fusing of the recurrence's fma into the rounding)
+    f32x4 v = st[q];
+    asm volatile("" : "+v"(v));
     vec4<T> hi, lo;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      hi[k] = from_f32<T>(st[q][k]);
-      lo[k] = from_f32<T>(st[q][k] - to_f32<T>(hi[k]));
+      hi[k] = from_f32<T>(v[k]);
+      lo[k] = from_f32<T>(v[k] - to_f32<T>(hi[k]));
     }
     const u32x2 hw = __builtin_bit_cast(u32x2, hi), lw = __builtin_bit_cast(u32x2, lo);
     const u32x2 give = odd ? hw : lw, keep = odd ? lw : hw;

@@ -12,10 +12,13 @@
 // running state in registers and streams the chunks.  Each step's local-state
 // load does not depend on the running state, so U chunks of loads are issued
 // before the U dependent FMAs and stores -- the loads run ahead of the FMA
-// chain.  Threads of a workgroup cover consecutive elements of one (b, h)
+// chain, and the next batch's loads are in flight while a batch is stored.
+// Threads of a workgroup cover consecutive elements of one (b, h)
 // state, so every load and store is a fully coalesced 16-byte access.
 // Pure streaming: HBM traffic per chunk is one read and one write of the
 // state, the roofline bound is HBM bandwidth.
+#include <type_traits>
+
 #include "ssd_device.h"
 #include "ssd_launch.h"
 #include "../../include/ssd.h"
@@ -27,13 +30,25 @@ namespace {
 constexpr int kUnroll = 8;
 
 template <typename S> struct StateIO;
+// Local states are read once.  Long chains read them with non-temporal loads
+// (a read-only stream of 16-byte nt loads reaches ~7.0 TB/s on MI355X against
+// ~6.3 TB/s for plain loads; K3 over 256 chunks gains ~3%); chains shorter
+// than two load batches use plain loads (nt loads made the 4-chunk C5 shape
+// 25% slower).  S_in is stored normally: chunk_scan reads it next and finds
+// part of it still cached.
+template <bool NT> __device__ __forceinline__ f32x4 load_state(const float* p) {
+  return NT ? __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(p)) : *reinterpret_cast<const f32x4*>(p);
+}
+
 template <> struct StateIO<float> {
-  __device__ static f32x4 load(const float* p) { return *reinterpret_cast<const f32x4*>(p); }
+  template <bool NT = false>
+  __device__ static f32x4 load(const float* p) { return load_state<NT>(p); }
   __device__ static void store(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
 };
 template <> struct StateIO<bf16> {
+  template <bool NT = false>
   __device__ static f32x4 load(const bf16* p) {
-    bf16x4 v = *reinterpret_cast<const bf16x4*>(p);
+    bf16x4 v = NT ? __builtin_nontemporal_load(reinterpret_cast<const bf16x4*>(p)) : *reinterpret_cast<const bf16x4*>(p);
     return f32x4{(float)v[0], (float)v[1], (float)v[2], (float)v[3]};
   }
   __device__ static void store(bf16* p, f32x4 v) {
@@ -41,6 +56,60 @@ template <> struct StateIO<bf16> {
     *reinterpret_cast<bf16x4*>(p) = o;
   }
 };
+
+// The recurrence over all chunks for one thread's 4 state elements, software
+// pipelined: the loads of the next kUnroll chunks are issued before the
+// current kUnroll chunks' stores and FMAs, so each thread always has a batch
+// of loads in flight (two register batches used in turn: no copies between
+// them, which would wait for the loads).  load(c) returns chunk c's local
+// state, store(c, v) writes S_in[c] = v; dec[c] is chunk c's decay.
+template <typename LoadF, typename StoreF>
+__device__ __forceinline__ f32x4 run_chain(int nchunks, const float* __restrict__ dec, f32x4 st, LoadF load,
+                                           StoreF store) {
+  f32x4 la[kUnroll], lb[kUnroll];
+  float da[kUnroll], db[kUnroll];
+  // In the main loop the loads are unconditional (past the last chunk they
+  // re-read it and the value is unused): with no branches around them the
+  // compiler's vmcnt waits count exactly, and waiting for one batch leaves the
+  // other in flight.  Chains shorter than two batches load only their chunks.
+  auto fetch = [&](int c0, f32x4* l, float* d, bool all) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (all || c0 + u < nchunks) {
+        const int c = min(c0 + u, nchunks - 1);
+        l[u] = all ? load(c, std::true_type()) : load(c, std::false_type());
+        d[u] = dec[c];
+      }
+    }
+  };
+  auto advance = [&](int c0, const f32x4* l, const float* d, bool all) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      if (all || c0 + u < nchunks) {
+        store(c0 + u, st);
+        st = st * d[u] + l[u];
+      }
+    }
+  };
+  int c0 = 0;
+  if (nchunks >= 2 * kUnroll) {
+    fetch(0, la, da, true);
+    for (; c0 + 2 * kUnroll <= nchunks; c0 += 2 * kUnroll) {
+      fetch(c0 + kUnroll, lb, db, true);
+      advance(c0, la, da, true);
+      fetch(c0 + 2 * kUnroll, la, da, true);
+      advance(c0 + kUnroll, lb, db, true);
+    }
+  } else {
+    fetch(0, la, da, false);
+  }
+  if (c0 < nchunks) {  // the last 1 .. 2 kUnroll - 1 chunks; la holds chunks c0 ..
+    fetch(c0 + kUnroll, lb, db, false);
+    advance(c0, la, da, false);
+    advance(c0 + kUnroll, lb, db, false);
+  }
+  return st;
+}
 
 template <typename S>
 __global__ __launch_bounds__(256) void state_passing_kernel(StatePassingArgs p) {
@@ -58,24 +127,10 @@ __global__ __launch_bounds__(256) void state_passing_kernel(StatePassingArgs p) 
 
   f32x4 st = p.init ? *reinterpret_cast<const f32x4*>(p.init + (int64_t)bh * PN + 4 * (int64_t)v)
                     : f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int c0 = 0; c0 < p.nchunks; c0 += kUnroll) {
-    f32x4 loc[kUnroll];
-    float d[kUnroll];
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (c0 + u < p.nchunks) {
-        loc[u] = StateIO<S>::load(base + (c0 + u) * cstride);
-        d[u] = dec[c0 + u];
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (c0 + u < p.nchunks) {
-        StateIO<S>::store(base + (c0 + u) * cstride, st);
-        st = st * d[u] + loc[u];
-      }
-    }
-  }
+  st = run_chain(
+      p.nchunks, dec, st,
+      [&](int c, auto nt) { return StateIO<S>::template load<decltype(nt)::value>(base + c * cstride); },
+      [&](int c, f32x4 val) { StateIO<S>::store(base + c * cstride, val); });
   if (p.final_state) *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * PN + 4 * (int64_t)v) = st;
 }
 
@@ -106,38 +161,31 @@ __global__ __launch_bounds__(256) void state_passing_split_kernel(StatePassingAr
                     : f32x4{0.f, 0.f, 0.f, 0.f};
   typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
   typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-  for (int c0 = 0; c0 < p.nchunks; c0 += kUnroll) {
-    f32x4 loc[kUnroll];
-    float d[kUnroll];
+  auto store_split = [&](int c, f32x4 val) {
+    // the split starts from the f32 state: opaque, so that the compiler cannot
+    // fuse the recurrence's fma with the rounding to T (one rounding instead of
+    // two would change hi in rare cases)
+    asm volatile("" : "+v"(val));
+    vec4<T> hi, lo;
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (c0 + u < p.nchunks) {
-        loc[u] = *reinterpret_cast<const f32x4*>(base + (c0 + u) * cstride);
-        d[u] = dec[c0 + u];
-      }
+    for (int k = 0; k < 4; ++k) {
+      hi[k] = from_f32<T>(val[k]);
+      lo[k] = from_f32<T>(val[k] - to_f32<T>(hi[k]));
     }
-#pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
-      if (c0 + u < p.nchunks) {
-        vec4<T> hi, lo;
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          hi[k] = from_f32<T>(st[k]);
-          lo[k] = from_f32<T>(st[k] - to_f32<T>(hi[k]));
-        }
-        const u32x2 hw = __builtin_bit_cast(u32x2, hi), lw = __builtin_bit_cast(u32x2, lo);
-        // even lane keeps its hi and receives the odd lane's hi; odd lane the reverse for lo
-        const u32x2 give = odd ? hw : lw, keep = odd ? lw : hw;
-        u32x2 got;
-        got[0] = (uint32_t)__builtin_amdgcn_mov_dpp((int)give[0], 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
-        got[1] = (uint32_t)__builtin_amdgcn_mov_dpp((int)give[1], 0xB1, 0xF, 0xF, false);
-        const u32x4 out = odd ? u32x4{got[0], got[1], keep[0], keep[1]} : u32x4{keep[0], keep[1], got[0], got[1]};
-        // the pair's 32 bytes start at the even lane's 16: hi at +0, lo at +16
-        *reinterpret_cast<u32x4*>(base + (c0 + u) * cstride) = out;
-        st = st * d[u] + loc[u];
-      }
-    }
-  }
+    const u32x2 hw = __builtin_bit_cast(u32x2, hi), lw = __builtin_bit_cast(u32x2, lo);
+    // even lane keeps its hi and receives the odd lane's hi; odd lane the reverse for lo
+    const u32x2 give = odd ? hw : lw, keep = odd ? lw : hw;
+    u32x2 got;
+    got[0] = (uint32_t)__builtin_amdgcn_mov_dpp((int)give[0], 0xB1, 0xF, 0xF, false);  // quad_perm 1,0,3,2
+    got[1] = (uint32_t)__builtin_amdgcn_mov_dpp((int)give[1], 0xB1, 0xF, 0xF, false);
+    const u32x4 out = odd ? u32x4{got[0], got[1], keep[0], keep[1]} : u32x4{keep[0], keep[1], got[0], got[1]};
+    // the pair's 32 bytes start at the even lane's 16: hi at +0, lo at +16
+    *reinterpret_cast<u32x4*>(base + c * cstride) = out;
+  };
+  st = run_chain(
+      p.nchunks, dec, st,
+      [&](int c, auto nt) { return StateIO<float>::template load<decltype(nt)::value>(base + c * cstride); },
+      store_split);
   if (p.final_state) *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * PN + 4 * (int64_t)v) = st;
 }
 
