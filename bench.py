@@ -57,12 +57,15 @@ def esize(dt):
     return torch.tensor([], dtype=dt).element_size()
 
 
-def kernel_model(cfg, state_dtype):
+def kernel_model(cfg, state_dtype, handover=None):
     """Algorithmic HBM bytes and MFMA flops per launch of each kernel.
 
     Bytes count every operand read once and every result written once at its
-    storage type (B and C per group, not per head).  Flops count useful work:
-    the causal triangle T_Q = Q(Q+1)/2 of the intra-chunk products.
+    storage type (B and C per group, not per head); the states entering each
+    chunk at the format K3 hands them to K4 in (``handover`` "f16s": 2 bytes
+    per state plus a 4-byte scale per state row; otherwise the state dtype,
+    the (hi, lo) pairs taking 4 bytes).  Flops count useful work: the causal
+    triangle T_Q = Q(Q+1)/2 of the intra-chunk products.
     """
     b, L, h, P, N, Q, g = cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.chunk, cfg.ngroups
     c = L // Q
@@ -73,6 +76,7 @@ def kernel_model(cfg, state_dtype):
     acs = b * h * c * Q * 4
     dec = b * h * c * 4
     st = b * c * h * P * N * ss
+    sin = b * c * h * (P * N * 2 + P * 4) if handover == "f16s" else st
     fin = b * h * P * N * 4 if cfg.final_state else 0
     init = b * h * P * N * 4 if cfg.init_state else 0
     TQ = Q * (Q + 1) // 2
@@ -82,10 +86,10 @@ def kernel_model(cfg, state_dtype):
         "chunk_cumsum": dict(bytes=a + acs + dec, flops=b * L * h),
         "chunk_prep": dict(bytes=2 * bc + cb_frag + bt_frag, flops=2 * b * c * g * TQ * N),
         "chunk_state": dict(bytes=x + bc + acs + st, flops=2 * b * c * h * Q * P * N),
-        "state_passing": dict(bytes=2 * st + dec + fin + init, flops=2 * b * c * h * P * N),
+        "state_passing": dict(bytes=st + sin + dec + fin + init, flops=2 * b * c * h * P * N),
         # K2 + K3 as the forward runs them: x in, S_in out; the local states are not counted
-        "chunk_state_passing": dict(bytes=x + bc + acs + dec + st + fin + init, flops=2 * b * c * h * (Q + 1) * P * N),
-        "chunk_scan": dict(bytes=x + 2 * bc + acs + st + x,
+        "chunk_state_passing": dict(bytes=x + bc + acs + dec + sin + fin + init, flops=2 * b * c * h * (Q + 1) * P * N),
+        "chunk_scan": dict(bytes=x + 2 * bc + acs + sin + x,
                            flops=b * c * h * (2 * TQ * N + 2 * TQ * P + 2 * Q * N * P)),
     }
 
@@ -261,6 +265,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--config", default=HEADLINE, choices=sorted(CONFIGS))
     ap.add_argument("--state-dtype", default="f32", choices=["f32", "bf16"])
+    ap.add_argument("--state-format", default=None, choices=["split", "f16s"],
+                    help="how f32 states reach chunk_scan (default: the library's choice, f16s at chunk 256)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=30)
     ap.add_argument("--layer", action="store_true",
@@ -299,7 +305,8 @@ def main():
 
     def step():
         return S.ssd_forward(X, A, B, C, cfg.chunk, initial_states=init,
-                             return_final_states=cfg.final_state, state_dtype=state_dtype)
+                             return_final_states=cfg.final_state, state_dtype=state_dtype,
+                             state_format=args.state_format)
 
     for _ in range(args.warmup):
         step()
@@ -323,8 +330,11 @@ def main():
     prep = S.chunk_prep(B, C, cfg.chunk)
     states = S.chunk_state(X, B, Acs, state_dtype=state_dtype, prep=prep)
     # as in ssd_forward: with prep (chunk 256, 16-bit inputs) and f32 states, K3
-    # hands S_in to K4 as 16-bit (hi, lo) pairs
-    split = cfg.dtype if (prep is not None and state_dtype == torch.float32) else None
+    # hands S_in to K4 as f16 rows with a power-of-two scale per row ("f16s"),
+    # or as 16-bit (hi, lo) pairs with --state-format split
+    split = None
+    if prep is not None and state_dtype == torch.float32:
+        split = cfg.dtype if args.state_format == "split" else "f16s"
     S_in, _ = S.state_passing(states, decay, init, split=split)
     # K3 is timed in place on its own buffers, re-applying the recurrence to
     # their contents on every launch: the same traffic and instructions (nothing
@@ -334,12 +344,13 @@ def main():
     # states that are no longer cached.
     nbuf = max(2, -(-512 * 2**20 // states.numel() // states.element_size()))
     sp_bufs = [states.clone() for _ in range(nbuf)]
+    sp_scales = torch.empty(states.shape[:4], dtype=torch.float32, device=dev) if split == "f16s" else None
     sp_next = [0]
 
     def sp_launch():
         buf = sp_bufs[sp_next[0] % nbuf]
         sp_next[0] += 1
-        return S.state_passing_(buf, decay, init, sp_final, split=split)
+        return S.state_passing_(buf, decay, init, sp_final, split=split, scales=sp_scales)
 
     sp_final = torch.empty(cfg.batch, cfg.nheads, cfg.headdim, cfg.dstate, device=dev) if cfg.final_state else None
     kfn = {
@@ -350,11 +361,12 @@ def main():
         "chunk_state_passing": lambda: S.chunk_state_passing(X, B, Acs, decay, prep=prep, initial_states=init,
                                                              return_final_states=cfg.final_state, split=split,
                                                              state_dtype=state_dtype),
-        "chunk_scan": lambda: S.chunk_scan(X, B, C, Acs, S_in, prep=prep, split=split is not None),
+        "chunk_scan": lambda: S.chunk_scan(X, B, C, Acs, S_in, prep=prep,
+                                           split="f16s" if split == "f16s" else split is not None),
     }
     if prep is None:
         del kfn["chunk_prep"]
-    model = kernel_model(cfg, state_dtype)
+    model = kernel_model(cfg, state_dtype, split if isinstance(split, str) else None)
     kernels = {}
     for name, fn in kfn.items():
         fn()
@@ -401,6 +413,7 @@ def main():
                    "batch": cfg.batch, "seqlen": cfg.seqlen, "nheads": cfg.nheads, "headdim": cfg.headdim,
                    "dstate": cfg.dstate, "chunk": cfg.chunk, "ngroups": cfg.ngroups,
                    "inputs": f"{DTYPE_NAMES[cfg.dtype]} X/B/C, f32 A", "state_storage": args.state_dtype,
+                   "state_handover": split if isinstance(split, str) else ("split" if split is not None else None),
                    "final_state": cfg.final_state, "initial_state": cfg.init_state},
         "device_ms_per_step": round(dev_ms, 5),
         "step_stats": stats,

@@ -41,21 +41,31 @@
 extern "C" {
 #endif
 
-#define SSD_ABI_VERSION 4
+#define SSD_ABI_VERSION 5
 
-/* Element types.  The two SPLIT values are a storage format of the per-chunk
- * states only: each f32 state as the 16-bit pair hi = round(v),
- * lo = round(v - hi) of the inputs' type, stored per 8 consecutive states as
- * [hi x8 | lo x8] (4 bytes per state, as f32).  ssd_state_passing writes it
- * from f32 local states; ssd_chunk_scan reads it, for 16-bit inputs of that
- * type at chunk 256 and dstate 64 / 128, as MFMA operands without converting
- * it.  ssd_forward uses it internally. */
+/* Element types.  The SPLIT and F16S values are storage formats of the
+ * per-chunk states only, both laid out in the f32 states buffer
+ * [b, c, h, P, N] (4 bytes per state):
+ *   SPLIT: each f32 state as the 16-bit pair hi = round(v), lo = round(v - hi)
+ *     of the inputs' type, stored per 8 consecutive states as [hi x8 | lo x8].
+ *   F16S: each state row p (N states) as N f16 values v / 2^e in the first half
+ *     of the row's f32 slots, and the scale 2^e (f32) in a separate array
+ *     state_scales [b, c, h, P]; e is chosen per row so that the row's largest
+ *     |v| lies in [2^14, 2^15] (f16's 11-bit significand; MR:155 itself stores
+ *     the states in float16).
+ * ssd_state_passing and ssd_chunk_state_passing write them from f32 local
+ * states; ssd_chunk_scan reads them, for 16-bit inputs at chunk 256 and
+ * dstate 64 / 128 (F16S with dstate 128 for the one-launch state chain), as
+ * MFMA operands without converting them.  ssd_forward hands the states to
+ * chunk_scan as F16S wherever that applies (state_dtype SSD_DTYPE_F32), or
+ * in the format state_dtype names. */
 enum {
   SSD_DTYPE_F32 = 0,
   SSD_DTYPE_BF16 = 1,
   SSD_DTYPE_F16 = 2,
   SSD_STATE_SPLIT_BF16 = 3,
   SSD_STATE_SPLIT_F16 = 4,
+  SSD_STATE_F16S = 5,
 };
 
 /* Status codes (negative: rejected on the host before any launch). */
@@ -141,8 +151,10 @@ int ssd_chunk_state(const ssd_dims* d, int dtype,
  * local state, on exit the state entering chunk c:
  *   S_in[0] = initial (or 0), S_in[c+1] = chunk_decay[c] S_in[c] + S_local[c].
  * Replaces the Python loop at MR:152-157.  final_states (optional) receives
- * the state after the last chunk, which MR computes and discards (MR:156). */
-int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype,
+ * the state after the last chunk, which MR computes and discards (MR:156).
+ * state_scales: [b, c, h, P] f32, written for SSD_STATE_F16S (NULL otherwise);
+ * the same argument of ssd_chunk_state_passing and ssd_chunk_scan. */
+int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, float* state_scales,
                       const float* chunk_decay, const float* initial_states,
                       float* final_states, void* stream);
 
@@ -162,8 +174,8 @@ int ssd_chunk_state_passing(const ssd_dims* d, int dtype,
                             const float* dt, const int64_t dt_strides[3],
                             const float* a_cumsum, const float* chunk_decay,
                             const void* prep, const float* initial_states,
-                            void* states, int state_dtype, float* final_states,
-                            void* stream);
+                            void* states, int state_dtype, float* state_scales,
+                            float* final_states, void* stream);
 
 /* Skip and gate of SSDLayer.forward (MR:116-118), applied by ssd_chunk_scan
  * to y in float32 before its single rounding to the output dtype:
@@ -190,6 +202,7 @@ int ssd_chunk_scan(const ssd_dims* d, int dtype,
                    const void* cmat, const int64_t c_strides[4],
                    const float* dt, const int64_t dt_strides[3],
                    const float* a_cumsum, const void* states, int state_dtype,
+                   const float* state_scales,
                    void* y, const int64_t y_strides[4],
                    const void* prep, const ssd_epilogue* epilogue, void* stream);
 

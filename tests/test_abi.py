@@ -123,23 +123,32 @@ def test_entry_points_reject_null_and_bad_strides_before_launch():
     assert lib.ssd_chunk_prep(ctypes.byref(big), 1, fake, bs4, fake, bs4, ctypes.c_void_p(0x100010), n, None) == -10
     assert lib.ssd_chunk_prep(ctypes.byref(big), 1, fake, bs4, fake, bs4, fake, n - 256, None) == -11
     # state passing: misaligned initial state
-    assert lib.ssd_state_passing(ctypes.byref(dims), fake, 0, fake, ctypes.c_void_p(0x100004), None, None) == -10
+    assert lib.ssd_state_passing(ctypes.byref(dims), fake, 0, None, fake, ctypes.c_void_p(0x100004), None, None) == -10
+    # the f16s format needs its scales array (and a shape the chunk-256 kernels take)
+    big256 = _lib.SSDDims(1, 512, 8, 64, 128, 1, 256)
+    assert lib.ssd_state_passing(ctypes.byref(big256), fake, 5, None, fake, None, None, None) == -1
+    assert lib.ssd_state_passing(ctypes.byref(big256), fake, 5, ctypes.c_void_p(0x100002), fake, None, None, None) == -10
+    small_n = _lib.SSDDims(1, 512, 8, 64, 32, 1, 256)
+    assert lib.ssd_state_passing(ctypes.byref(small_n), fake, 5, fake, fake, None, None, None) == -7
     # chunk_state + state_passing in one entry point: the same operand checks, plus the decay and
     # the split format's type (the inputs' own)
     csp = lib.ssd_chunk_state_passing
-    assert csp(ctypes.byref(dims), 1, None, s4, fake, bs4, None, None, fake, fake, None, None, fake, 0, None, None) == -1
-    assert csp(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, fake, None, None, None, fake, 0, None, None) == -1
-    assert csp(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, fake, fake, None, None, None, 0, None, None) == -1
+    assert csp(ctypes.byref(dims), 1, None, s4, fake, bs4, None, None, fake, fake, None, None, fake, 0, None, None, None) == -1
+    assert csp(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, fake, None, None, None, fake, 0, None, None, None) == -1
+    assert csp(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, fake, fake, None, None, None, 0, None, None, None) == -1
     assert csp(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, fake, fake, None, None,
-               ctypes.c_void_p(0x100004), 0, None, None) == -10
-    assert csp(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, fake, fake, None, None, fake, 0,
+               ctypes.c_void_p(0x100004), 0, None, None, None) == -10
+    assert csp(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, fake, fake, None, None, fake, 0, None,
                ctypes.c_void_p(0x100004), None) == -10
     # split pairs of the other 16-bit type, or of f32 inputs: unsupported
     assert csp(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, fake, fake, None, None, fake,
-               _lib.STATE_SPLIT_F16, None, None) == -5
+               _lib.STATE_SPLIT_F16, None, None, None) == -5
     assert csp(ctypes.byref(dims), 0, fake, s4, fake, bs4, None, None, fake, fake, None, None, fake,
-               _lib.STATE_SPLIT_BF16, None, None) == -5
-    assert csp(ctypes.byref(dims), 1, fake, bad, fake, bs4, None, None, fake, fake, None, None, fake, 0, None, None) == -9
+               _lib.STATE_SPLIT_BF16, None, None, None) == -5
+    # the f16s format needs its scales array
+    assert csp(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, fake, fake, None, None, fake,
+               _lib.STATE_F16S, None, None, None) == -1
+    assert csp(ctypes.byref(dims), 1, fake, bad, fake, bs4, None, None, fake, fake, None, None, fake, 0, None, None, None) == -9
 
 
 def test_python_op_refuses_cpu_tensors_instead_of_falling_back():

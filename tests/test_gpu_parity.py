@@ -106,6 +106,35 @@ def test_k3_state_passing(state_dtype, init, nc):
     assert_close(final, rfinal, 1e-5)
 
 
+@pytest.mark.parametrize("N", [64, 128])
+@pytest.mark.parametrize("init", [False, True])
+def test_k3_f16s_format(N, init):
+    """state_passing's f16s handover: row p of each state holds N f16 values v
+    and the scales array a power of two s with max|v| in [2^14, 2^15]; v s is
+    the f32 S_in to within f16 rounding (half an f16 ulp of the row's scale)."""
+    say("k3 f16s", N, init)
+    g = torch.Generator().manual_seed(N)
+    local = torch.randn(2, 5, 3, 64, N, generator=g) * torch.logspace(-3, 3, 64).reshape(1, 1, 1, 64, 1)
+    decay = torch.rand(2, 3, 5, generator=g)
+    s0 = torch.randn(2, 3, 64, N, generator=g) if init else None
+    dev = lambda t: None if t is None else t.to(DEV)  # noqa: E731
+    ref, rfinal = S.state_passing(local.to(DEV), dev(decay), dev(s0))
+    got, final = S.state_passing(local.to(DEV), dev(decay), dev(s0), split="f16s")
+    torch.cuda.synchronize()
+    assert torch.equal(final, rfinal)
+    v = got.states.view(torch.float16)[..., :N].double().cpu()
+    sc = got.scales.double().cpu()
+    assert torch.equal(torch.exp2(torch.log2(sc).round()), sc)   # powers of two
+    vmax = v.abs().amax(-1)
+    live = vmax > 0
+    # (a row maximum just below 2^15 may round up to it)
+    bad = live & ~((vmax >= 2.0 ** 14) & (vmax <= 2.0 ** 15))
+    assert not bad.any(), f"row maxima outside [2^14, 2^15]: {vmax[bad][:8].tolist()} scales {sc[bad][:8].tolist()}"
+    dec = v * sc[..., None]
+    r = ref.double().cpu()
+    assert ((dec - r).abs() <= sc[..., None] * 2.0 ** 3 * (1 + 1e-9)).all()   # half an f16 ulp at 2^14..2^15
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("Q", [64, 128, 256])
 @pytest.mark.parametrize("N", [16, 32, 64, 128])
@@ -199,7 +228,9 @@ def test_forward_equals_kernel_by_kernel(dtype, N, h, g, use_dt):
     cfg, inp = small_case(dtype, 256, N, b=4, nc=16, h=h, g=g)
     d = to_dev(inp)
     dt = torch.rand(4, 16 * 256, h, device=DEV) + 0.5 if use_dt else None
-    Y, final = S.ssd_forward(d["X"], d["A"], d["B"], d["C"], 256, dt=dt, return_final_states=True)
+    # the forward handing S_in over as (hi, lo) pairs: the same values as f32 S_in
+    Y, final = S.ssd_forward(d["X"], d["A"], d["B"], d["C"], 256, dt=dt, return_final_states=True,
+                             state_format="split")
     Acs, dec = S.chunk_cumsum(d["A"], 256)
     st = S.chunk_state(d["X"], d["B"], Acs, dt=dt)
     S_in, fin = S.state_passing(st, dec)
@@ -211,12 +242,18 @@ def test_forward_equals_kernel_by_kernel(dtype, N, h, g, use_dt):
     # the forward's own K3 -> K4 hand-over: S_in stored as (hi, lo) pairs
     S_sp, fin_sp = S.state_passing(st, dec, split=dtype)
     Ys = S.chunk_scan(d["X"], d["B"], d["C"], Acs, S_sp, dt=dt, prep=prep, split=True)
+    # the default forward hands S_in over as f16 rows with per-row scales
+    Yf, final_f = S.ssd_forward(d["X"], d["A"], d["B"], d["C"], 256, dt=dt, return_final_states=True)
+    S_f, fin_f = S.state_passing(st, dec, split="f16s")
+    Yfk = S.chunk_scan(d["X"], d["B"], d["C"], Acs, S_f, dt=dt, prep=prep, split="f16s")
     torch.cuda.synchronize()
     assert torch.equal(Y, Yk)
     assert torch.equal(Yp, Yk)
     assert torch.equal(Ys, Yk)
     assert torch.equal(final, fin)
     assert torch.equal(fin_sp, fin)
+    assert torch.equal(Yf, Yfk)
+    assert torch.equal(final_f, fin) and torch.equal(fin_f, fin)
 
 
 # ---------------------------------------------------------------------------

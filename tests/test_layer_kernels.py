@@ -197,8 +197,9 @@ def test_ssd_layer_equals_its_kernels_one_by_one(dtype, N, g, h):
     X, dto, Acs, dec = S.layer_prep(x, dt, dev["conv_w"], dev["conv_b"], dev["dt_bias"], dev["A_log"], Q, h)
     prep = S.chunk_prep(B, C, Q)
     st = S.chunk_state(X, B, Acs, dt=dto, prep=prep)
-    S_in, _ = S.state_passing(st, dec, split=dtype)
-    yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dto, prep=prep, split=True, D=dev["D"], z=z.reshape(b, L, h, P))
+    # the layer hands S_in to chunk_scan as f16 rows with per-row scales
+    S_in, _ = S.state_passing(st, dec, split="f16s")
+    yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dto, prep=prep, split="f16s", D=dev["D"], z=z.reshape(b, L, h, P))
     torch.cuda.synchronize()
     assert torch.equal(y, yk.reshape(b, L, h * P))
 

@@ -8,8 +8,10 @@ state_passing finishes.  The shapes here have 192-256 chains (one per CU on
 a 256-CU MI355X), 640 (three per CU) or 300-360 (the mixed plan).  It must give exactly what the two kernels
 give one after the other: ssd_forward against the public per-kernel entry
 points, bit for bit (Y and the final state), with and without dt and an
-initial state, both 16-bit types, both dstates, several groups.  The
-per-kernel path itself is held to the oracle by the parity tests."""
+initial state, both 16-bit types, both dstates, several groups, for both
+formats in which state_passing hands f32 states to chunk_scan (hi/lo pairs,
+"split"; f16 rows with a power-of-two scale per row, "f16s", the default).
+The per-kernel path itself is held to the oracle by the parity tests."""
 
 import pytest
 import torch
@@ -39,6 +41,30 @@ def takes_chain(chains):
     return chain_plan(chains) is not None
 
 
+FORMATS = ["split", "f16s"]
+
+
+def kernels_one_by_one(X, A, B, C, dt, init, fmt, Q=256):
+    """K1, K0, K2, K3 (handing S_in over in `fmt`), K4 through their own entry points."""
+    Acs, decay = S.chunk_cumsum(A, Q)
+    prep = S.chunk_prep(B, C, Q)
+    st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
+    S_in, fk = S.state_passing(st, decay, initial_states=init, split=X.dtype if fmt == "split" else "f16s")
+    Yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dt, prep=prep, split=True if fmt == "split" else "f16s")
+    return Yk, fk
+
+
+def handover_bytes(S_in, fmt):
+    """The bytes of handed-over states that carry data: all of them for
+    "split"; for "f16s" (S.F16SStates) the f16 half of each row and the row
+    scales."""
+    if fmt != "f16s":
+        return S_in.view(torch.uint8)
+    N = S_in.states.shape[-1]
+    return torch.cat([S_in.states.view(torch.float16)[..., :N].contiguous().view(torch.uint8).reshape(-1),
+                      S_in.scales.contiguous().view(torch.uint8).reshape(-1)])
+
+
 def case(dtype, b, L, h, P, N, g, seed):
     gen = torch.Generator().manual_seed(seed)
     X = torch.randn(b, L, h, P, generator=gen).to(dtype)
@@ -50,71 +76,63 @@ def case(dtype, b, L, h, P, N, g, seed):
     return [t.to(DEV) for t in (X, A, B, C, dt, init)]
 
 
+@pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("N,g,h", [(128, 1, 96), (64, 2, 128), (128, 4, 112)])
 @pytest.mark.parametrize("with_dt,with_init", [(True, True), (False, False), (True, False)])
-def test_forward_equals_kernels_one_by_one(dtype, N, g, h, with_dt, with_init):
+def test_forward_equals_kernels_one_by_one(dtype, N, g, h, with_dt, with_init, fmt):
     b, L, P, Q = 2, 1280, 64, 256
-    print("CASE chain", dtype, N, g, h, with_dt, with_init, flush=True)
+    print("CASE chain", dtype, N, g, h, with_dt, with_init, fmt, flush=True)
     if not takes_chain(b * h):
         pytest.skip("this device's CU count sends the shape to chunk_state then state_passing")
     X, A, B, C, dt, init = case(dtype, b, L, h, P, N, g, seed=N + g + h)
     dt = dt if with_dt else None
     init = init if with_init else None
-    Y, final = S.ssd_forward(X, A, B, C, Q, dt=dt, initial_states=init, return_final_states=True)
-
-    Acs, decay = S.chunk_cumsum(A, Q)
-    prep = S.chunk_prep(B, C, Q)
-    st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
-    S_in, fk = S.state_passing(st, decay, initial_states=init, split=dtype)
-    Yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dt, prep=prep, split=True)
+    Y, final = S.ssd_forward(X, A, B, C, Q, dt=dt, initial_states=init, return_final_states=True, state_format=fmt)
+    Yk, fk = kernels_one_by_one(X, A, B, C, dt, init, fmt, Q)
     torch.cuda.synchronize()
     assert torch.equal(final, fk)
     assert torch.equal(Y, Yk)
 
 
-def test_single_chunk_and_many_chains():
+@pytest.mark.parametrize("fmt", FORMATS)
+def test_single_chunk_and_many_chains(fmt):
     """One chunk per chain (the loop body runs once) and more chains than the
     GPU holds at once."""
     for (b, L, h) in [(2, 256, 100), (4, 512, 160)]:
-        print("CASE chain shape", b, L, h, flush=True)
+        print("CASE chain shape", b, L, h, fmt, flush=True)
         if not takes_chain(b * h):
             pytest.skip("this device's CU count sends the shape to chunk_state then state_passing")
         X, A, B, C, dt, init = case(torch.bfloat16, b, L, h, 64, 128, 1, seed=L + h)
-        Y, final = S.ssd_forward(X, A, B, C, 256, dt=dt, initial_states=init, return_final_states=True)
-        Acs, decay = S.chunk_cumsum(A, 256)
-        prep = S.chunk_prep(B, C, 256)
-        st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
-        S_in, fk = S.state_passing(st, decay, initial_states=init, split=torch.bfloat16)
-        Yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dt, prep=prep, split=True)
+        Y, final = S.ssd_forward(X, A, B, C, 256, dt=dt, initial_states=init, return_final_states=True,
+                                 state_format=fmt)
+        Yk, fk = kernels_one_by_one(X, A, B, C, dt, init, fmt)
         torch.cuda.synchronize()
         assert torch.equal(final, fk)
         assert torch.equal(Y, Yk)
 
 
+@pytest.mark.parametrize("fmt", FORMATS)
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("b,h,L,g", [(2, 160, 1280, 1), (3, 120, 2048, 4), (1, 300, 256, 2), (2, 150, 4096, 2)])
-def test_mixed_plan_equals_kernels_one_by_one(dtype, b, h, L, g):
+def test_mixed_plan_equals_kernels_one_by_one(dtype, b, h, L, g, fmt):
     """Whole chains, segments of the remaining chains (ragged last segment
     with 5 chunks, a single chunk, 16 chunks), state_passing over those
     chains only, with an initial state and the final state."""
-    print("CASE chain mixed", dtype, b, h, L, g, flush=True)
+    print("CASE chain mixed", dtype, b, h, L, g, fmt, flush=True)
     if chain_plan(b * h) != "mixed":
         pytest.skip("this device's CU count does not give the mixed plan for this shape")
     X, A, B, C, dt, init = case(dtype, b, L, h, 64, 128, g, seed=b * h + L)
-    Y, final = S.ssd_forward(X, A, B, C, 256, dt=dt, initial_states=init, return_final_states=True)
-    Acs, decay = S.chunk_cumsum(A, 256)
-    prep = S.chunk_prep(B, C, 256)
-    st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
-    S_in, fk = S.state_passing(st, decay, initial_states=init, split=dtype)
-    Yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dt, prep=prep, split=True)
+    Y, final = S.ssd_forward(X, A, B, C, 256, dt=dt, initial_states=init, return_final_states=True,
+                             state_format=fmt)
+    Yk, fk = kernels_one_by_one(X, A, B, C, dt, init, fmt)
     torch.cuda.synchronize()
     assert torch.equal(final, fk)
     assert torch.equal(Y, Yk)
 
 
 @pytest.mark.parametrize("b,h,L", [(2, 128, 1280), (2, 160, 1280), (1, 24, 512)])
-@pytest.mark.parametrize("split", [torch.bfloat16, None])
+@pytest.mark.parametrize("split", [torch.bfloat16, "f16s", None])
 def test_chunk_state_passing_entry_point(b, h, L, split):
     """ssd_chunk_state_passing (whole chains, the mixed plan, or chunk_state
     then state_passing, by shape) against the two entry points it stands for,
@@ -128,4 +146,5 @@ def test_chunk_state_passing_entry_point(b, h, L, split):
     S_ref, f_ref = S.state_passing(st, decay, initial_states=init, split=split)
     torch.cuda.synchronize()
     assert torch.equal(final, f_ref)
-    assert torch.equal(S_in.view(torch.uint8), S_ref.view(torch.uint8))
+    fmt = "f16s" if split == "f16s" else "split"
+    assert torch.equal(handover_bytes(S_in, fmt), handover_bytes(S_ref, fmt))

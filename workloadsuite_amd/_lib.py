@@ -15,9 +15,10 @@ import torch  # noqa: F401  -- must precede the CDLL, see module docstring
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssd.so")
 
-SSD_ABI_VERSION = 4
+SSD_ABI_VERSION = 5
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 STATE_SPLIT_BF16, STATE_SPLIT_F16 = 3, 4  # f32 states as 16-bit (hi, lo) pairs
+STATE_F16S = 5  # f32 states as f16 rows with a power-of-two scale per row
 
 # Every symbol include/ssd.h declares.
 EXPORTS = (
@@ -71,11 +72,11 @@ _SIGNATURES = {
     "ssd_chunk_prep_bytes": (ctypes.c_size_t, [_dims_p]),
     "ssd_chunk_prep": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, ctypes.c_size_t, _vp]),
     "ssd_chunk_state": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _int, _vp, _vp]),
-    "ssd_state_passing": (_int, [_dims_p, _vp, _int, _vp, _vp, _vp, _vp]),
+    "ssd_state_passing": (_int, [_dims_p, _vp, _int, _vp, _vp, _vp, _vp, _vp]),
     "ssd_chunk_state_passing": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _vp, _vp,
-                                       _vp, _int, _vp, _vp]),
+                                       _vp, _int, _vp, _vp, _vp]),
     "ssd_chunk_scan": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
-                              _vp, _vp, _int, _vp, _i64p, _vp, _epi_p, _vp]),
+                              _vp, _vp, _int, _vp, _vp, _i64p, _vp, _epi_p, _vp]),
     "ssd_forward": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                            _vp, _vp, _i64p, _vp, _vp, ctypes.c_size_t, _int, _vp]),
     "ssd_decode_step": (_int, [_dims_p, _int, _vp, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _i64p,

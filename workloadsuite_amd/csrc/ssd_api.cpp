@@ -42,6 +42,9 @@ int split_of(int state_dtype) {
 
 bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// A handover format of f32 states (SPLIT or F16S): stored in the f32 layout.
+bool f32_layout(int state_dtype) { return split_of(state_dtype) != 0 || state_dtype == SSD_STATE_F16S; }
+
 int check_dims_impl(const ssd_dims* d, int dtype) {
   if (!d) return SSD_ERR_NULL_POINTER;
   if (d->batch < 1 || d->seqlen < 1 || d->nheads < 1 || d->headdim < 1 || d->dstate < 1 ||
@@ -101,7 +104,7 @@ int hip_status(hipError_t e) { return e == hipSuccess ? SSD_OK : (int)e; }
 size_t round_up(size_t v) { return (v + kWsAlign - 1) / kWsAlign * kWsAlign; }
 
 struct WsLayout {
-  size_t acs, decay, states, prep, total;
+  size_t acs, decay, states, scales, prep, total;
 };
 
 // chunk_prep's outputs only exist for the persistent kernels' shapes
@@ -125,7 +128,10 @@ WsLayout ws_layout(const ssd_dims* d, int state_dtype) {
   w.acs = 0;
   w.decay = round_up(bhc * (size_t)d->chunk * sizeof(float));
   w.states = w.decay + round_up(bhc * sizeof(float));
-  w.prep = w.states + round_up(bhc * (size_t)d->headdim * d->dstate * elem_size(state_dtype));
+  w.scales = w.states + round_up(bhc * (size_t)d->headdim * d->dstate * elem_size(state_dtype));
+  // the row scales of f16s-handed-over states (only with f32 states and the chunk-256 kernels' shapes)
+  const size_t scales = state_dtype == SSD_DTYPE_F32 && prep_shape(d) ? bhc * (size_t)d->headdim * sizeof(float) : 0;
+  w.prep = w.scales + round_up(scales);
   w.total = w.prep + prep_bytes(d);
   return w;
 }
@@ -290,7 +296,8 @@ CumsumArgs make_cumsum_args(const ssd_dims* d, const float* a, const int64_t a_s
 int run_state_passing(const ssd_dims* d, int dtype, const ChunkStateArgs& sa, const StatePassingArgs& pa,
                       int state_dtype, hipStream_t s) {
   int rc;
-  const ssd::ChainPlan plan = pa.split_dtype ? ssd::chunk_state_chain_plan(sa, dtype) : ssd::ChainPlan{0, 1, 1};
+  ssd::ChainPlan plan = (pa.split_dtype || pa.f16s) ? ssd::chunk_state_chain_plan(sa, dtype) : ssd::ChainPlan{0, 1, 1};
+  if (pa.f16s && sa.dstate != 128) plan = ssd::ChainPlan{0, 1, 1};  // the chain's f16s store needs d_state 128
   if (plan.nfull > 0) {
     // K2 and K3 as one launch: the local states stay in registers (same bits);
     // chains beyond nfull leave local states that K3 finishes
@@ -306,6 +313,16 @@ int run_state_passing(const ssd_dims* d, int dtype, const ChunkStateArgs& sa, co
   }
   if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, state_dtype, s)))) return rc;
   return hip_status(ssd::launch_state_passing(pa, state_dtype, s));
+}
+
+// The format in which the forward hands f32 states from K3 to K4: 0 (plain
+// f32 or bf16 states), SSD_STATE_F16S or a SPLIT value; only the chunk-256
+// persistent chunk_scan reads the handover formats.
+int handover_format(const ssd_dims* d, int dtype, int state_dtype, const ChunkScanArgs& ca) {
+  if (!f32_layout(state_dtype) && state_dtype != SSD_DTYPE_F32) return 0;
+  if (!prep_applies(d, dtype) || !ssd::chunk_scan_persistent_supported(ca, dtype)) return 0;
+  if (state_dtype == SSD_DTYPE_F32 || state_dtype == SSD_STATE_F16S) return SSD_STATE_F16S;
+  return state_dtype;
 }
 
 int run_core(const ssd_dims* d, int dtype, const CumsumArgs* k1, const void* x, const int64_t x_strides[4],
@@ -336,14 +353,23 @@ int run_core(const ssd_dims* d, int dtype, const CumsumArgs* k1, const void* x, 
   } else if (k1) {
     if ((rc = hip_status(ssd::launch_chunk_cumsum(*k1, s)))) return rc;
   }
-  // f32 states for the chunk-256 chunk_scan: K3 writes them as its hi/lo operand pairs
+  // f32 states for the chunk-256 chunk_scan: K3 (or the state chain) hands
+  // them over as f16 with per-row scales (the default), or as its hi/lo
+  // operand pairs when state_dtype asks for that format
   StatePassingArgs pa = make_sp_args(d, states, decay, initial_states, final_states);
-  if (state_dtype == SSD_DTYPE_F32 && prep_applies(d, dtype) && ssd::chunk_scan_persistent_supported(ca, dtype)) {
+  const int handover = handover_format(d, dtype, state_dtype, ca);
+  if (handover == SSD_STATE_F16S) {
+    pa.f16s = 1;
+    ca.f16s = true;
+    pa.sscale = reinterpret_cast<float*>(ws + w.scales);
+    ca.sscale = pa.sscale;
+  } else if (handover) {
     pa.split_dtype = dtype;
     ca.presplit = true;
   }
-  if ((rc = run_state_passing(d, dtype, sa, pa, state_dtype, s))) return rc;
-  return hip_status(ssd::launch_chunk_scan(ca, dtype, state_dtype, s));
+  const int sd = f32_layout(state_dtype) ? SSD_DTYPE_F32 : state_dtype;
+  if ((rc = run_state_passing(d, dtype, sa, pa, sd, s))) return rc;
+  return hip_status(ssd::launch_chunk_scan(ca, dtype, sd, s));
 }
 
 // ---- the layer around the core ----
@@ -485,7 +511,9 @@ const char* ssd_strerror(int status) {
     case SSD_ERR_BAD_SHAPE: return "every dimension must be >= 1";
     case SSD_ERR_SEQLEN_NOT_DIVISIBLE: return "seqlen must be a multiple of the chunk size";
     case SSD_ERR_HEADS_NOT_DIVISIBLE: return "n_heads must be divisible by n_groups";
-    case SSD_ERR_UNSUPPORTED_DTYPE: return "unsupported dtype (f32, bf16, f16; bf16 states need 16-bit inputs)";
+    case SSD_ERR_UNSUPPORTED_DTYPE:
+      return "unsupported dtype or state format (f32, bf16, f16; bf16 states and the SPLIT / F16S formats need "
+             "16-bit inputs, and the formats chunk 256 with dstate 64 or 128)";
     case SSD_ERR_UNSUPPORTED_HEADDIM: return "unsupported head_dim (must be 64)";
     case SSD_ERR_UNSUPPORTED_DSTATE: return "unsupported d_state (16, 32, 64 or 128)";
     case SSD_ERR_UNSUPPORTED_CHUNK: return "unsupported chunk size (64, 128 or 256)";
@@ -504,6 +532,7 @@ int ssd_check_dims(const ssd_dims* d, int dtype) { return check_dims_impl(d, dty
 
 size_t ssd_workspace_bytes(const ssd_dims* d, int state_dtype) {
   if (check_dims_impl(d, SSD_DTYPE_BF16) != SSD_OK) return 0;
+  if (f32_layout(state_dtype)) state_dtype = SSD_DTYPE_F32;
   if (state_dtype != SSD_DTYPE_F32 && state_dtype != SSD_DTYPE_BF16) return 0;
   return ws_layout(d, state_dtype).total;
 }
@@ -555,60 +584,76 @@ int ssd_chunk_state(const ssd_dims* d, int dtype, const void* x, const int64_t x
   return hip_status(ssd::launch_chunk_state(p, dtype, state_dtype, (hipStream_t)stream));
 }
 
-int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, const float* chunk_decay,
-                      const float* initial_states, float* final_states, void* stream) {
+int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, float* state_scales,
+                      const float* chunk_decay, const float* initial_states, float* final_states, void* stream) {
   int rc = check_dims_impl(d, SSD_DTYPE_BF16);
   if (rc) return rc;
   const int split = split_of(state_dtype);
-  if (state_dtype != SSD_DTYPE_F32 && state_dtype != SSD_DTYPE_BF16 && !split) return SSD_ERR_UNSUPPORTED_DTYPE;
-  if (!states || !chunk_decay) return SSD_ERR_NULL_POINTER;
+  const bool f16s = state_dtype == SSD_STATE_F16S;
+  if (state_dtype != SSD_DTYPE_F32 && state_dtype != SSD_DTYPE_BF16 && !split && !f16s)
+    return SSD_ERR_UNSUPPORTED_DTYPE;
+  if (f16s && d->dstate != 64 && d->dstate != 128) return SSD_ERR_UNSUPPORTED_DSTATE;
+  if (!states || !chunk_decay || (f16s && !state_scales)) return SSD_ERR_NULL_POINTER;
+  if (f16s && (reinterpret_cast<uintptr_t>(state_scales) & 3u)) return SSD_ERR_MISALIGNED;
   if (!aligned16(states) || (initial_states && !aligned16(initial_states)) ||
       (final_states && !aligned16(final_states)))
     return SSD_ERR_MISALIGNED;
   StatePassingArgs p = make_sp_args(d, states, chunk_decay, initial_states, final_states);
   p.split_dtype = split;
-  return hip_status(ssd::launch_state_passing(p, split ? SSD_DTYPE_F32 : state_dtype, (hipStream_t)stream));
+  p.f16s = f16s ? 1 : 0;
+  p.sscale = f16s ? state_scales : nullptr;
+  return hip_status(ssd::launch_state_passing(p, f32_layout(state_dtype) ? SSD_DTYPE_F32 : state_dtype,
+                                              (hipStream_t)stream));
 }
 
 int ssd_chunk_state_passing(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4],
                             const void* bmat, const int64_t b_strides[4], const float* dt,
                             const int64_t dt_strides[3], const float* a_cumsum, const float* chunk_decay,
                             const void* prep, const float* initial_states, void* states, int state_dtype,
-                            float* final_states, void* stream) {
+                            float* state_scales, float* final_states, void* stream) {
   int rc = check_dims_impl(d, dtype);
   if (rc) return rc;
   const int split = split_of(state_dtype);
-  if (split ? split != dtype : !valid_state_dtype(dtype, state_dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+  const bool f16s = state_dtype == SSD_STATE_F16S;
+  if (f16s ? (dtype == SSD_DTYPE_F32 || (d->dstate != 64 && d->dstate != 128))
+           : split ? split != dtype : !valid_state_dtype(dtype, state_dtype))
+    return SSD_ERR_UNSUPPORTED_DTYPE;
   if ((rc = check_vec_operand(x, x_strides, 4, dtype))) return rc;
   if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
-  if (!a_cumsum || !chunk_decay || !states) return SSD_ERR_NULL_POINTER;
+  if (!a_cumsum || !chunk_decay || !states || (f16s && !state_scales)) return SSD_ERR_NULL_POINTER;
   if (!aligned16(states) || (initial_states && !aligned16(initial_states)) ||
-      (final_states && !aligned16(final_states)))
+      (final_states && !aligned16(final_states)) || (f16s && (reinterpret_cast<uintptr_t>(state_scales) & 3u)))
     return SSD_ERR_MISALIGNED;
   if (prep && (reinterpret_cast<uintptr_t>(prep) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
   ChunkStateArgs sa = make_state_args(d, x, x_strides, bmat, b_strides, dt, dt_strides, a_cumsum, states);
   if (prep_applies(d, dtype)) sa.btf = prep_btf(d, prep);
   StatePassingArgs pa = make_sp_args(d, states, chunk_decay, initial_states, final_states);
   pa.split_dtype = split;
-  return run_state_passing(d, dtype, sa, pa, split ? SSD_DTYPE_F32 : state_dtype, (hipStream_t)stream);
+  pa.f16s = f16s ? 1 : 0;
+  pa.sscale = f16s ? state_scales : nullptr;
+  return run_state_passing(d, dtype, sa, pa, f32_layout(state_dtype) ? SSD_DTYPE_F32 : state_dtype,
+                           (hipStream_t)stream);
 }
 
 int ssd_chunk_scan(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4],
                    const void* bmat, const int64_t b_strides[4], const void* cmat,
                    const int64_t c_strides[4], const float* dt, const int64_t dt_strides[3],
-                   const float* a_cumsum, const void* states, int state_dtype, void* y,
-                   const int64_t y_strides[4], const void* prep, const ssd_epilogue* epilogue,
+                   const float* a_cumsum, const void* states, int state_dtype, const float* state_scales,
+                   void* y, const int64_t y_strides[4], const void* prep, const ssd_epilogue* epilogue,
                    void* stream) {
   int rc = check_dims_impl(d, dtype);
   if (rc) return rc;
   const int split = split_of(state_dtype);
-  if (!valid_state_dtype(dtype, state_dtype) && !(split && split == dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+  const bool f16s = state_dtype == SSD_STATE_F16S;
+  if (!valid_state_dtype(dtype, state_dtype) && !(split && split == dtype) && !(f16s && dtype != SSD_DTYPE_F32))
+    return SSD_ERR_UNSUPPORTED_DTYPE;
   if ((rc = check_vec_operand(x, x_strides, 4, dtype))) return rc;
   if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
   if ((rc = check_vec_operand(cmat, c_strides, 4, dtype))) return rc;
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
-  if (!a_cumsum || !states) return SSD_ERR_NULL_POINTER;
+  if (!a_cumsum || !states || (f16s && !state_scales)) return SSD_ERR_NULL_POINTER;
+  if (f16s && (reinterpret_cast<uintptr_t>(state_scales) & 3u)) return SSD_ERR_MISALIGNED;
   if ((rc = check_output(y, y_strides, dtype))) return rc;
   if ((rc = check_epilogue(epilogue, dtype))) return rc;
   if (prep && (reinterpret_cast<uintptr_t>(prep) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
@@ -616,12 +661,15 @@ int ssd_chunk_scan(const ssd_dims* d, int dtype, const void* x, const int64_t x_
                                    states, y, y_strides);
   set_epilogue(p, epilogue);
   if (prep_applies(d, dtype)) p.cbf = prep_cbf(prep);
-  if (split) {
-    // only the chunk-256 kernel reads split states
+  if (split || f16s) {
+    // only the chunk-256 kernel reads the handover formats
     if (!prep_applies(d, dtype) || !ssd::chunk_scan_persistent_supported(p, dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
-    p.presplit = true;
+    p.presplit = split != 0;
+    p.f16s = f16s;
+    p.sscale = f16s ? state_scales : nullptr;
   }
-  return hip_status(ssd::launch_chunk_scan(p, dtype, split ? SSD_DTYPE_F32 : state_dtype, (hipStream_t)stream));
+  return hip_status(ssd::launch_chunk_scan(p, dtype, f32_layout(state_dtype) ? SSD_DTYPE_F32 : state_dtype,
+                                           (hipStream_t)stream));
 }
 
 int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_strides[4], const float* a,
@@ -632,10 +680,13 @@ int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_str
                 size_t workspace_bytes, int state_dtype, void* stream) {
   int rc = check_dims_impl(d, dtype);
   if (rc) return rc;
-  if (!valid_state_dtype(dtype, state_dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+  const int split = split_of(state_dtype);
+  if (!valid_state_dtype(dtype, state_dtype) && !(split && split == dtype) &&
+      !(state_dtype == SSD_STATE_F16S && dtype != SSD_DTYPE_F32))
+    return SSD_ERR_UNSUPPORTED_DTYPE;
   if (!workspace) return SSD_ERR_NULL_POINTER;
   if ((reinterpret_cast<uintptr_t>(workspace) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
-  const WsLayout w = ws_layout(d, state_dtype);
+  const WsLayout w = ws_layout(d, f32_layout(state_dtype) ? SSD_DTYPE_F32 : state_dtype);
   if (workspace_bytes < w.total) return SSD_ERR_WORKSPACE_TOO_SMALL;
   // Validate every operand before the first launch, so a bad argument never
   // leaves a partially computed result behind.

@@ -77,6 +77,7 @@ struct ScanArgs32 {
   const void* states;
   void* y;
   const float* cbf;  // chunk_prep's CB^T fragments, or null
+  const float* sscale;  // F16S: the row scales of the states [b, c, h, P]
   int cb16;          // ... rounded to T (the epilogue variant)
   int presplit;      // f32 S_in already stored as [hi x8 | lo x8] pairs
   const float* dskip;  // epilogue: skip weights [h], or null
@@ -88,6 +89,14 @@ struct ScanArgs32 {
 struct Item {
   int b, c, h, grp;
 };
+
+// State storage tag: f32 states handed over as f16 with a power-of-two scale
+// per state row p (SSD_STATE_F16S): row p of an item (N f32 slots) holds N
+// f16 values in its first half; the row scales are a separate [b, c, h, P]
+// array.
+struct f16s_t {};
+template <typename S> struct StateElem { typedef S type; };
+template <> struct StateElem<f16s_t> { typedef f16 type; };
 
 // CB^T blocks of one 32-token s block (two 16x16 sub-tiles st) as MFMA D
 // fragments: f32, or rounded to T where the registers are needed elsewhere
@@ -119,11 +128,15 @@ template <typename T, typename S, int NK, bool HAS_DT, bool PREP, bool EPI>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void chunk_scan_q256_kernel(ScanArgs32 p) {
   constexpr int N = 32 * NK;                      // dstate (64 or 128)
-  constexpr bool SPLIT = sizeof(S) == 4;          // f32 states become a hi/lo pair
+  constexpr bool F16S = std::is_same<S, f16s_t>::value;  // f16 rows with a per-row scale
+  constexpr bool SPLIT = std::is_same<S, float>::value;  // f32 states become a hi/lo pair
+  typedef typename StateElem<S>::type SE;          // element type of the stored states
+  // global layout: row stride GRS and item stride of the states, in SE elements
+  constexpr int GRS = F16S ? 2 * N : N;
   // S_in rows in LDS: RB bytes, PPR 16-byte pieces, unpadded; piece c of row
   // r sits at slot c ^ ssw(r), which spreads the 16 rows that one operand
   // read touches over distinct banks.  One 64-lane copy moves RPD rows.
-  constexpr int RB = N * (int)sizeof(S);
+  constexpr int RB = N * (int)sizeof(SE);
   constexpr int PPR = RB / 16;
   constexpr int RPD = 1024 / RB;
   constexpr int SCOPIES = kP / RPD / kNW;         // S_in copies per wave and item
@@ -140,6 +153,8 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   // of the blocks below the diagonal factors as exp(Acs[l] - Acs[r]) * G[s]).
   __shared__ __attribute__((aligned(16))) float ar[kNW][kQ];
   __shared__ __attribute__((aligned(16))) float wt[kNW][2][kQ];
+  // F16S: the per-row scales of S_in, current and next item
+  __shared__ __attribute__((aligned(16))) float scl[2][F16S ? kP : 4];
 
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   __builtin_assume(wave < kNW);  // lets the tile-range tests below fold
@@ -186,7 +201,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   // S_in copy: lane k fills slot k % PPR of row RPD d + k / PPR, i.e. reads
   // piece (k % PPR) ^ ssw(row); the row's ssw depends on d only through the
   // wave (RPD d = RPD wave mod 16).
-  const int scopy = (lane / PPR) * N + ((lane % PPR) ^ ssw(wave * RPD + lane / PPR)) * (16 / (int)sizeof(S));
+  const int scopy = (lane / PPR) * GRS + ((lane % PPR) ^ ssw(wave * RPD + lane / PPR)) * (16 / (int)sizeof(SE));
 
 
   // ---- global -> LDS copy of one item's x, S_in, Acs (and dt) into buffer b ----
@@ -194,6 +209,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   // so that no generic -> LDS pointer conversion is needed per copy).
   const uint32_t xr_lds = lds_offset(&xr[0][0]), sr_lds = lds_offset(&sr[0][0]);
   const uint32_t ar_lds = lds_offset(&ar[0][0]), dr_lds = lds_offset(&dr[0][0]);
+  const uint32_t scl_lds = lds_offset(&scl[0][0]);
 
   // Part `part` (0..3) of one item's copy: x block rows 64 part + 8 wave ..,
   // S_in rows 16 part + wave and + 8; part 0 also copies Acs (and dt).  The
@@ -212,11 +228,15 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
       dma16_at(xg + (int64_t)(8 * blk) * p.sxl, xr_lds + (uint32_t)(b * kQ * kP * (int)sizeof(T) + blk * 1024));
     }
     // S_in: copy d = wave + 8 part moves rows RPD d .. RPD d + RPD - 1 (1 KB).
+    const int64_t item = ((int64_t)r.b * p.nchunks + r.c) * p.nheads + r.h;
     if (part < SCOPIES) {
-      const S* sg = reinterpret_cast<const S*>(p.states) +
-                    (((int64_t)r.b * p.nchunks + r.c) * p.nheads + r.h) * (int64_t)(kP * N) + scopy;
+      const SE* sg = reinterpret_cast<const SE*>(p.states) + item * (int64_t)(kP * GRS) + scopy;
       const int d = wave + kNW * part;
-      dma16_at(sg + d * RPD * N, sr_lds + (uint32_t)(b * kP * RB + d * 1024));
+      dma16_at(sg + d * RPD * GRS, sr_lds + (uint32_t)(b * kP * RB + d * 1024));
+    }
+    if constexpr (F16S) {
+      // the item's 64 row scales (256 contiguous bytes)
+      if (part == 1 && wave == 0) dma4_at(p.sscale + item * kP + lane, scl_lds + (uint32_t)(b * kP * 4));
     }
     if (part == 0) {
       const float* ag = p.acs + (((int64_t)r.b * p.nheads + r.h) * p.nchunks + r.c) * kQ;
@@ -246,7 +266,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   // S_in: each 32-byte pair of pieces (8 states) becomes [hi x8 | lo x8] of T
   // in place, unless state_passing already stored it so; bf16 S_in with f16
   // inputs: converted to f16 in place.
-  constexpr bool kBf16ToF16 = !SPLIT && !std::is_same<S, T>::value;
+  constexpr bool kBf16ToF16 = !SPLIT && !F16S && !std::is_same<S, T>::value;
   const bool must_convert = SPLIT ? !p.presplit : kBf16ToF16;
   auto convert = [&](int b) __attribute__((always_inline)) {
     if constexpr (SPLIT) {
@@ -271,10 +291,10 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     } else if constexpr (kBf16ToF16) {
       for (int u = tid; u < kP * PPR; u += kThreads) {
         unsigned char* pr = sr[b] + 16 * u;
-        const frag8<S> v = *reinterpret_cast<const frag8<S>*>(pr);
+        const frag8<SE> v = *reinterpret_cast<const frag8<SE>*>(pr);
         frag8<T> o;
 #pragma unroll
-        for (int k = 0; k < 8; ++k) o[k] = from_f32<T>(to_f32<S>(v[k]));
+        for (int k = 0; k < 8; ++k) o[k] = from_f32<T>(to_f32<SE>(v[k]));
         *reinterpret_cast<frag8<T>*>(pr) = o;
       }
     }
@@ -283,6 +303,33 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   // ---- per-group registers: C fragments of both tiles and their CB^T blocks ----
   frag8<T> cf[2][NK];
   CbStep<T, EPI> cbc[kNPair];
+  // F16S: the off-diagonal product runs on f16 MFMAs, so each C row l of the
+  // two tiles is held as f16 scaled by a power of two 2^-e (its largest
+  // element then lies in [2^14, 2^15): bf16 values convert exactly), and
+  // cs[t] = 2^e undoes it with the decay factor of row l.
+  float cs[2] = {1.f, 1.f};
+  auto c_to_f16 = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float m = 0.f;
+#pragma unroll
+      for (int kc = 0; kc < NK; ++kc)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(to_f32<T>(cf[t][kc][j])));
+      // the row's 4 lane groups (lanes i, i + 16, i + 32, i + 48)
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
+      cs[t] = __builtin_ldexpf(1.f, e);
+#pragma unroll
+      for (int kc = 0; kc < NK; ++kc) {
+        f16x8 h;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) h[j] = (f16)__builtin_ldexpf(to_f32<T>(cf[t][kc][j]), -e);
+        cf[t][kc] = __builtin_bit_cast(frag8<T>, h);
+      }
+    }
+  };
   auto load_group = [&](int it) __attribute__((always_inline)) {
     int lane_o = lane;
     asm volatile("" : "+v"(lane_o));
@@ -309,6 +356,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
             cbc[k].v[0] = v.lo;
             cbc[k].v[1] = v.hi;
           }
+          if constexpr (F16S && !std::is_same<T, f16>::value) c_to_f16();
           return;
         }
       }
@@ -317,6 +365,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
       for (int k = 0; k < kNPair; ++k)
 #pragma unroll
         for (int st = 0; st < 2; ++st) cbc[k].set(st, cb[(k * 2 + st) * 64]);
+      if constexpr (F16S && !std::is_same<T, f16>::value) c_to_f16();
       return;
     }
     // One 32-token s block (two 16x16 sub-tiles) per step; every row lies in
@@ -348,6 +397,7 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if constexpr (F16S && !std::is_same<T, f16>::value) c_to_f16();
   };
 
   // ---- one item from LDS buffer b into packed y registers ----
@@ -386,6 +436,12 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
 #pragma unroll
       for (int kc = 0; kc < NK; ++kc) {
         const unsigned char* q = sbuf + 16 * pt * RB + 256 * (kc / NKB);
+        if constexpr (F16S) {
+          const f16x8 a = *reinterpret_cast<const f16x8*>(q + sbase[kc % NKB][0]);
+          acc[0][pt] = mma(a, __builtin_bit_cast(f16x8, cf[0][kc]), acc[0][pt]);
+          acc[1][pt] = mma(a, __builtin_bit_cast(f16x8, cf[1][kc]), acc[1][pt]);
+          continue;
+        }
         const frag8<T> hi = *reinterpret_cast<const frag8<T>*>(q + sbase[kc % NKB][0]);
         acc[0][pt] = mma(hi, cf[0][kc], acc[0][pt]);
         acc[1][pt] = mma(hi, cf[1][kc], acc[1][pt]);
@@ -397,11 +453,25 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
       }
       __builtin_amdgcn_sched_barrier(0);  // bound how far LDS reads are hoisted (register pressure)
     }
+    if constexpr (F16S) {
+      // rows p of the off-diagonal tiles carry their S_in row scale, columns
+      // l the C row scale and exp(Acs[l])
+      f32x4 sc[4];
 #pragma unroll
-    for (int s2 = 0; s2 < 2; ++s2) {
-      const float e = __builtin_amdgcn_exp2f(al[s2]);
+      for (int pt = 0; pt < 4; ++pt) sc[pt] = *reinterpret_cast<const f32x4*>(&scl[b][16 * pt + 4 * g]);
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt) acc[s2][pt] *= e;
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const float e = __builtin_amdgcn_exp2f(al[s2]) * cs[s2];
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) acc[s2][pt] *= sc[pt] * e;
+      }
+    } else {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const float e = __builtin_amdgcn_exp2f(al[s2]);
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) acc[s2][pt] *= e;
+      }
     }
     if constexpr (EPI) {
       if (p.z) {
@@ -627,6 +697,7 @@ ScanArgs32 narrow(const ChunkScanArgs& a) {
   n.states = a.states;
   n.y = a.y;
   n.cbf = a.cbf;
+  n.sscale = a.sscale;
   n.cb16 = a.cb16 ? 1 : 0;
   n.presplit = a.presplit ? 1 : 0;
   n.dskip = a.dskip;
@@ -684,6 +755,12 @@ bool chunk_scan_persistent_supported(const ChunkScanArgs& a, int dtype) {
 }
 
 hipError_t launch_chunk_scan_persistent(const ChunkScanArgs& a, int dtype, int state_dtype, hipStream_t stream) {
+  if (a.f16s) {
+    if (!a.sscale) return hipErrorInvalidValue;
+    if (dtype == SSD_DTYPE_BF16) return launch_ts<bf16, f16s_t>(a, stream);
+    if (dtype == SSD_DTYPE_F16) return launch_ts<f16, f16s_t>(a, stream);
+    return hipErrorInvalidValue;
+  }
   if (state_dtype == SSD_DTYPE_F32) {
     if (dtype == SSD_DTYPE_BF16) return launch_ts<bf16, float>(a, stream);
     if (dtype == SSD_DTYPE_F16) return launch_ts<f16, float>(a, stream);

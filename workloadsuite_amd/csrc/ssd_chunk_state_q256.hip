@@ -310,16 +310,20 @@ hipError_t launch_ts(const ChunkStateArgs& a, hipStream_t stream) {
 // chunks' f32 local states, exactly as chunk_state would, for state_passing
 // to finish: with 1.25 chains per CU the whole chains take one workgroup slot
 // of every CU and the segments the second.
-template <typename T, int NK, bool HAS_DT>
+template <typename T, int NK, bool HAS_DT, bool F16S>
 __global__ __launch_bounds__(64 * kNW) __attribute__((amdgpu_waves_per_eu(4)))
 void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan plan) {
   constexpr int N = 32 * NK;
   constexpr int NTILE = N / 16;
   constexpr int PTW = NTILE / 2;
+  static_assert(!F16S || NTILE == kNW, "the f16s store has one n tile per wave");
   __shared__ __attribute__((aligned(1024))) T xr[2][kQ * kP];
   __shared__ __attribute__((aligned(16))) float ar[2][kQ];
   __shared__ __attribute__((aligned(16))) float dr[HAS_DT ? 2 : 1][HAS_DT ? kQ : 4];
   __shared__ __attribute__((aligned(16))) float wr[kQ];
+  // F16S: each wave's largest |state| per row p over its n tile, for the
+  // state entering the current chunk and the next one ([parity][p][wave])
+  __shared__ __attribute__((aligned(16))) float rmx[2][F16S ? kP : 1][kNW];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -412,6 +416,48 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
     float* sg = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (int64_t)(kP * N);
     *reinterpret_cast<u32x4*>(sg + srow + 16 * N * q) = out;
   };
+  // F16S (SSD_STATE_F16S): S_in[c] as f16 rows with a power-of-two scale per
+  // row p (row p's N f16 values in the first half of its f32 slots, the scale
+  // in sp.sscale[b, c, h, p]).  The row's largest |state| spans all waves (one
+  // n tile each): every wave publishes its own per-row maximum into rmx[par]
+  // once the state is final, and after the next barrier each lane reads the 8
+  // maxima of its 4 rows.
+  auto publish_rowmax = [&](int par) __attribute__((always_inline)) {
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) {
+      float m = fmaxf(fmaxf(fabsf(st[q][0]), fabsf(st[q][1])), fmaxf(fabsf(st[q][2]), fabsf(st[q][3])));
+      // across the lane groups g (lanes i, i + 16, i + 32, i + 48): swap with
+      // the neighbouring 16-lane row, then with the other 32-lane half
+      {
+        const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+        m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+        const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+        m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+      }
+      if (g == 0) rmx[par][16 * (pt0 + q) + i][wave] = m;
+    }
+  };
+  auto store_sin_f16s = [&](int c, int par) __attribute__((always_inline)) {
+    float* item = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (int64_t)(kP * N);
+#pragma unroll
+    for (int q = 0; q < PTW; ++q) {
+      const int row = 16 * (pt0 + q) + i;
+      const f32x4 m0 = *reinterpret_cast<const f32x4*>(&rmx[par][row][0]);
+      const f32x4 m1 = *reinterpret_cast<const f32x4*>(&rmx[par][row][4]);
+      const float m = fmaxf(fmaxf(fmaxf(m0[0], m0[1]), fmaxf(m0[2], m0[3])),
+                            fmaxf(fmaxf(m1[0], m1[1]), fmaxf(m1[2], m1[3])));
+      const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
+      f32x4 v = st[q];
+      asm volatile("" : "+v"(v));  // from the f32 state (no fusing of the recurrence into the rounding)
+      f16x4 hv;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hv[k] = (f16)__builtin_ldexpf(v[k], -e);
+      *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;
+      if (wave == 0 && g == 0)
+        sp.sscale[(((int64_t)b * p.nchunks + c) * p.nheads + h) * kP + row] = __builtin_ldexpf(1.f, e);
+    }
+  };
+
   // a segment's local state of chunk c (f32, chunk_state's layout)
   auto store_local = [&](int c, int q) __attribute__((always_inline)) {
     float* sg = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (int64_t)(kP * N);
@@ -426,6 +472,9 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
   }
 #pragma unroll
   for (int m = 0; m < kXBlocks / kNW; ++m) issue_copy_part(c0, 0, m);
+  if constexpr (F16S) {
+    if (!local) publish_rowmax(c0 & 1);
+  }
   dma_wait();
   __syncthreads();
   tabulate(0);
@@ -466,6 +515,11 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
       for (int q = 0; q < PTW; ++q) st[q] = acc[q];
 #pragma unroll
       for (int q = 0; q < PTW; ++q) store_local(c, q);
+    } else if constexpr (F16S) {
+      store_sin_f16s(c, c & 1);
+#pragma unroll
+      for (int q = 0; q < PTW; ++q) st[q] = st[q] * dec + acc[q];
+      publish_rowmax((c + 1) & 1);
     } else {
 #pragma unroll
       for (int q = 0; q < PTW; ++q) store_sin(c, q);
@@ -487,7 +541,10 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
 template <typename T, int NK>
 hipError_t launch_chain_nk(const ChunkStateArgs& a, const StatePassingArgs& sp, const ChainPlan& plan,
                            hipStream_t stream) {
-  auto kern = a.dt ? chunk_state_chain_kernel<T, NK, true> : chunk_state_chain_kernel<T, NK, false>;
+  constexpr bool kF16S = 32 * NK / 16 == kNW;  // the f16s store needs one n tile per wave (d_state 128)
+  if (sp.f16s && (!kF16S || !sp.sscale)) return hipErrorInvalidValue;
+  auto kern = sp.f16s ? (a.dt ? chunk_state_chain_kernel<T, NK, true, kF16S> : chunk_state_chain_kernel<T, NK, false, kF16S>)
+                      : (a.dt ? chunk_state_chain_kernel<T, NK, true, false> : chunk_state_chain_kernel<T, NK, false, false>);
   const int64_t rest = (int64_t)a.batch * a.nheads - plan.nfull;
   const unsigned grid = (unsigned)(plan.nfull + rest * plan.seg_per_chain);
   kern<<<dim3(grid), dim3(64 * kNW), 0, stream>>>(a, sp, plan);
@@ -547,7 +604,8 @@ ChainPlan chunk_state_chain_plan(const ChunkStateArgs& a, int dtype) {
 hipError_t launch_chunk_state_chain(const ChunkStateArgs& a, const StatePassingArgs& sp, const ChainPlan& plan,
                                     int dtype, hipStream_t stream) {
   const int64_t chains = (int64_t)a.batch * a.nheads;
-  if (!chunk_state_chain_supported(a, dtype) || sp.split_dtype != dtype || plan.nfull < 1 || plan.nfull > chains ||
+  if (!chunk_state_chain_supported(a, dtype) || (sp.f16s ? sp.split_dtype != 0 : sp.split_dtype != dtype) ||
+      plan.nfull < 1 || plan.nfull > chains ||
       plan.seg_per_chain < 1 || plan.seg_len < 1 || (int64_t)plan.seg_per_chain * plan.seg_len < a.nchunks ||
       plan.nfull + (chains - plan.nfull) * plan.seg_per_chain > INT_MAX)
     return hipErrorInvalidValue;

@@ -61,6 +61,10 @@ struct StatePassingArgs {
   // 0, or SSD_DTYPE_BF16 / F16: f32 S_in is written as chunk_scan's hi/lo
   // operand pairs of that type (chunk-256 forward path only)
   int split_dtype = 0;
+  // S_in written as f16 with a power-of-two scale per state row
+  // (SSD_STATE_F16S, in place in the f32 layout; chunk-256 forward path only)
+  int f16s = 0;
+  float* sscale = nullptr;  // f16s: the row scales [b, c, h, P]
   // chains (b * nheads + h) [bh_begin, bh_begin + bh_count) only; bh_count 0: all
   int bh_begin = 0, bh_count = 0;
 };
@@ -82,6 +86,8 @@ struct ChunkScanArgs {
   const float* cbf = nullptr;  // optional chunk_prep CB^T fragments (persistent kernel)
   bool cb16 = false;           // ... rounded to the input type (the epilogue variant reads those)
   bool presplit = false;       // f32 states already split by state_passing (split_dtype)
+  bool f16s = false;           // states in the SSD_STATE_F16S format (state_passing's f16s output)
+  const float* sscale = nullptr;  // ... and their row scales [b, c, h, P]
   // optional epilogue: y = (y + dskip[h] x) * silu(z)
   const float* dskip = nullptr;  // [h]
   const void* z = nullptr;       // [b, L, h, P], unit stride over P

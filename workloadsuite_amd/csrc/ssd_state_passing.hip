@@ -63,16 +63,16 @@ template <> struct StateIO<bf16> {
 // of loads in flight (two register batches used in turn: no copies between
 // them, which would wait for the loads).  load(c) returns chunk c's local
 // state, store(c, v) writes S_in[c] = v; dec[c] is chunk c's decay.
-template <typename LoadF, typename StoreF>
-__device__ __forceinline__ f32x4 run_chain(int nchunks, const float* __restrict__ dec, f32x4 st, LoadF load,
-                                           StoreF store) {
-  f32x4 la[kUnroll], lb[kUnroll];
+template <typename V, typename LoadF, typename StoreF>
+__device__ __forceinline__ V run_chain(int nchunks, const float* __restrict__ dec, V st, LoadF load,
+                                       StoreF store) {
+  V la[kUnroll], lb[kUnroll];
   float da[kUnroll], db[kUnroll];
   // In the main loop the loads are unconditional (past the last chunk they
   // re-read it and the value is unused): with no branches around them the
   // compiler's vmcnt waits count exactly, and waiting for one batch leaves the
   // other in flight.  Chains shorter than two batches load only their chunks.
-  auto fetch = [&](int c0, f32x4* l, float* d, bool all) __attribute__((always_inline)) {
+  auto fetch = [&](int c0, V* l, float* d, bool all) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (all || c0 + u < nchunks) {
@@ -82,7 +82,7 @@ __device__ __forceinline__ f32x4 run_chain(int nchunks, const float* __restrict_
       }
     }
   };
-  auto advance = [&](int c0, const f32x4* l, const float* d, bool all) __attribute__((always_inline)) {
+  auto advance = [&](int c0, const V* l, const float* d, bool all) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       if (all || c0 + u < nchunks) {
@@ -189,6 +189,97 @@ __global__ __launch_bounds__(256) void state_passing_split_kernel(StatePassingAr
   if (p.final_state) *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * PN + 4 * (int64_t)v) = st;
 }
 
+// The maximum of m over each aligned group of G lanes (G = 8 or 16, within
+// one DPP row), with DPP moves (no LDS round trip): two quad permutations,
+// then the half-row and row mirrors.
+template <int G>
+__device__ __forceinline__ float row_max(float m) {
+  static_assert(G == 8 || G == 16, "lane group");
+  auto dpp = [](float v, int ctrl) __attribute__((always_inline)) {
+    switch (ctrl) {
+      case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad 1,0,3,2
+      case 1: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));   // quad 2,3,0,1
+      case 2: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));  // row_half_mirror
+      default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)); // row_mirror
+    }
+  };
+  m = fmaxf(m, dpp(m, 0));
+  m = fmaxf(m, dpp(m, 1));
+  m = fmaxf(m, dpp(m, 2));
+  if constexpr (G == 16) m = fmaxf(m, dpp(m, 3));
+  return m;
+}
+
+// f32 states handed to the chunk-256 chunk_scan as f16 with a power-of-two
+// scale per state row (SSD_STATE_F16S), the f16 values written in place in
+// the f32 layout: row p of an item (N f32 slots) gets its N f16 values,
+// v / 2^e, in its first half, and 2^e goes to sscale[item][p]; e is chosen
+// so that the row's largest |v| lies in [2^14, 2^15].  Each thread owns 8
+// consecutive states of a row (two 16-byte loads per chunk, one 16-byte
+// store); the N/8 threads of a row (one wave holds whole rows) find the row's
+// largest magnitude with DPP moves.  Every load of a row precedes, in the
+// wave's instruction order, the stores into that row, so the in-place writes
+// never overtake a read.  The recurrence and final_state stay f32.
+template <int N>
+__global__ __launch_bounds__(256) void state_passing_f16s_kernel(StatePassingArgs p) {
+  constexpr int TPR = N / 8;  // threads per row
+  const int64_t PN = (int64_t)p.headdim * N;
+  const int vec_per_bh = (int)(PN / 8);
+  const int blocks_per_bh = (vec_per_bh + 255) / 256;
+  const int bh = p.bh_begin + (int)blockIdx.x / blocks_per_bh;
+  const int v = (blockIdx.x % blocks_per_bh) * 256 + threadIdx.x;
+  if (v >= vec_per_bh) return;  // vec_per_bh is a multiple of 256: whole waves leave together
+  const int h = bh % p.nheads, b = bh / p.nheads;
+  const int row = v / TPR, col = 8 * (v % TPR);
+
+  float* base = reinterpret_cast<float*>(p.states) + ((int64_t)b * p.nchunks * p.nheads + h) * PN;
+  const int64_t cstride = (int64_t)p.nheads * PN;
+  const float* dec = p.decay + (int64_t)bh * p.nchunks;
+  float* elem = base + 8 * (int64_t)v;                       // this thread's 8 f32 states
+  f16* hrow = reinterpret_cast<f16*>(base + (int64_t)row * N) + col;  // its 8 f16 slots
+  // the row's scale: sscale[b, c, h, row], chunks p.nheads * headdim apart
+  float* srow = p.sscale + ((int64_t)b * p.nchunks * p.nheads + h) * p.headdim + row;
+  const int64_t sstride = (int64_t)p.nheads * p.headdim;
+
+  f32x8 st;
+  if (p.init) {
+    st.lo = *reinterpret_cast<const f32x4*>(p.init + (int64_t)bh * PN + 8 * (int64_t)v);
+    st.hi = *reinterpret_cast<const f32x4*>(p.init + (int64_t)bh * PN + 8 * (int64_t)v + 4);
+  } else {
+    st = f32x8{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  }
+  auto store_f16s = [&](int c, f32x8 val) {
+    asm volatile("" : "+v"(val));  // from the f32 state (no fusing of the recurrence into the rounding)
+    float m = 0.f;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(val[k]));
+    m = row_max<TPR>(m);
+    const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
+    f16x8 hv;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) hv[k] = (f16)__builtin_ldexpf(val[k], -e);
+    *reinterpret_cast<f16x8*>(hrow + c * 2 * cstride) = hv;
+    if (col == 0) srow[c * sstride] = __builtin_ldexpf(1.f, e);
+  };
+  auto load8f = [&](int c, auto nt) {
+    const f32x4* q = reinterpret_cast<const f32x4*>(elem + c * cstride);
+    f32x8 r;
+    if constexpr (decltype(nt)::value) {
+      r.lo = __builtin_nontemporal_load(q);
+      r.hi = __builtin_nontemporal_load(q + 1);
+    } else {
+      r.lo = q[0];
+      r.hi = q[1];
+    }
+    return r;
+  };
+  st = run_chain(p.nchunks, dec, st, load8f, store_f16s);
+  if (p.final_state) {
+    *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * PN + 8 * (int64_t)v) = st.lo;
+    *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * PN + 8 * (int64_t)v + 4) = st.hi;
+  }
+}
+
 }  // namespace
 
 hipError_t launch_state_passing(const StatePassingArgs& a, int state_dtype, hipStream_t stream) {
@@ -196,6 +287,15 @@ hipError_t launch_state_passing(const StatePassingArgs& a, int state_dtype, hipS
   const int64_t all = (int64_t)a.batch * a.nheads;
   if (a.bh_begin < 0 || a.bh_count < 0 || a.bh_begin + (int64_t)a.bh_count > all) return hipErrorInvalidValue;
   const int64_t chains = a.bh_count > 0 ? a.bh_count : all - a.bh_begin;
+  if (a.f16s) {
+    if (state_dtype != SSD_DTYPE_F32 || a.split_dtype != 0 || !a.sscale || (PN / 8) % 256 != 0)
+      return hipErrorInvalidValue;
+    const dim3 grid((unsigned)(chains * ((PN / 8 + 255) / 256)));
+    if (a.dstate == 128) state_passing_f16s_kernel<128><<<grid, 256, 0, stream>>>(a);
+    else if (a.dstate == 64) state_passing_f16s_kernel<64><<<grid, 256, 0, stream>>>(a);
+    else return hipErrorInvalidValue;
+    return hipGetLastError();
+  }
   if (a.split_dtype != 0) {
     if (state_dtype != SSD_DTYPE_F32 || PN % 8 != 0) return hipErrorInvalidValue;
     if (PN % 256 != 0) return hipErrorInvalidValue;  // whole waves per (b, h)

@@ -28,6 +28,7 @@ as the reference harness runs it under ``torch.inference_mode()``.
 from __future__ import annotations
 
 import ctypes
+from typing import NamedTuple
 
 import torch
 
@@ -48,14 +49,49 @@ __all__ = [
     "ssd_layer",
     "workspace_bytes",
     "SSDError",
+    "F16SStates",
 ]
 
 SSDError = _lib.SSDError
 
 _DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16, torch.float16: _lib.DTYPE_F16}
 _STATE_DTYPES = {torch.float32: _lib.DTYPE_F32, torch.bfloat16: _lib.DTYPE_BF16}
-# f32 states stored as 16-bit (hi, lo) pairs of the inputs' type
-_SPLIT_STATES = {torch.bfloat16: _lib.STATE_SPLIT_BF16, torch.float16: _lib.STATE_SPLIT_F16}
+# f32 states stored as 16-bit (hi, lo) pairs of the inputs' type, or ("f16s")
+# as f16 rows with a power-of-two scale per row
+_SPLIT_STATES = {torch.bfloat16: _lib.STATE_SPLIT_BF16, torch.float16: _lib.STATE_SPLIT_F16,
+                 "f16s": _lib.STATE_F16S}
+
+
+class F16SStates(NamedTuple):
+    """States handed to chunk_scan as f16 rows with a power-of-two scale per
+    row (SSD_STATE_F16S): ``states`` [b, c, h, P, N] float32 storage whose
+    rows hold N f16 values in their first half, ``scales`` [b, c, h, P]
+    float32; state[..., p, n] = f16 value * scales[..., p]."""
+    states: torch.Tensor
+    scales: torch.Tensor
+
+    def decode(self) -> torch.Tensor:
+        N = self.states.shape[-1]
+        return self.states.view(torch.float16)[..., :N].float() * self.scales[..., None]
+
+
+def _handover(state_format, dtype, state_dtype):
+    """state_dtype code for ssd_forward: the storage of the per-chunk states
+    and, for f32 states, the format K3 hands them to K4 in (None: the
+    library's choice, f16 rows with per-row scales where the chunk-256 kernels
+    run; "split": hi/lo pairs of the inputs' type; "f16s")."""
+    sd = _STATE_DTYPES.get(state_dtype)
+    if sd is None:
+        raise ValueError(f"unsupported state dtype {state_dtype}")
+    if state_format is None:
+        return sd
+    if state_dtype != torch.float32 or dtype == torch.float32:
+        raise ValueError("state_format needs float32 states and 16-bit inputs")
+    if state_format == "split":
+        return _SPLIT_STATES[dtype]
+    if state_format == "f16s":
+        return _lib.STATE_F16S
+    raise ValueError(f"unknown state_format {state_format!r}")
 
 
 def _device_check(*ts):
@@ -169,13 +205,16 @@ def workspace_bytes(batch, seqlen, nheads, headdim, dstate, ngroups, chunk_size,
 
 
 def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
-                return_final_states=False, state_dtype=torch.float32):
+                return_final_states=False, state_dtype=torch.float32, state_format=None):
     """Chunked SSD forward (MR:123-162) on the HIP device.
 
     Returns Y, or (Y, final_states) with ``return_final_states``.
     ``state_dtype`` is the storage type of the per-chunk states between the
     kernels (float32, or bfloat16 for 16-bit inputs); the recurrence itself
-    always runs in float32.
+    always runs in float32.  ``state_format`` (float32 states, 16-bit inputs):
+    how chunk_scan receives them -- None (library default: f16 rows with a
+    power-of-two scale per row where the chunk-256 kernels run), "split"
+    (hi/lo pairs of the inputs' type) or "f16s".
     """
     b, L, h, P, g, N = _shape_check(X, A, B, C, chunk_size, dt, initial_states)
     dev = _device_check(X, A, B, C, dt, initial_states)
@@ -189,9 +228,7 @@ def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
     init = _f32_contig(initial_states)
     Y = torch.empty((b, L, h, P), dtype=X.dtype, device=dev)
     final = torch.empty((b, h, P, N), dtype=torch.float32, device=dev) if return_final_states else None
-    sd = _STATE_DTYPES.get(state_dtype)
-    if sd is None:
-        raise ValueError(f"unsupported state dtype {state_dtype}")
+    sd = _handover(state_format, X.dtype, state_dtype)
     ws_n = lib.ssd_workspace_bytes(ctypes.byref(d), sd)
     ws = torch.empty(ws_n, dtype=torch.uint8, device=dev)
     rc = lib.ssd_forward(ctypes.byref(d), _DTYPES[X.dtype],
@@ -205,7 +242,7 @@ def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
 
 
 def ssd_forward_noalloc(X, A, B, C, chunk_size, dt=None, initial_states=None,
-                        return_final_states=False, state_dtype=torch.float32):
+                        return_final_states=False, state_dtype=torch.float32, state_format=None):
     """``ssd_forward`` through the C ABI's ``ssd_forward_noalloc``: the library
     takes its workspace from a device array it keeps per device instead of a
     buffer allocated here (for callers that cannot allocate: graph capture,
@@ -217,9 +254,7 @@ def ssd_forward_noalloc(X, A, B, C, chunk_size, dt=None, initial_states=None,
     dev = _device_check(X, A, B, C, dt, initial_states)
     lib = _lib.load()
     d = _dims(b, L, h, P, N, g, chunk_size)
-    sd = _STATE_DTYPES.get(state_dtype)
-    if sd is None:
-        raise ValueError(f"unsupported state dtype {state_dtype}")
+    sd = _handover(state_format, X.dtype, state_dtype)
     X = _vec_operand(X.detach())
     Bm = _vec_operand(B.detach())
     Cm = _vec_operand(C.detach())
@@ -325,19 +360,22 @@ def state_passing(states, chunk_decay, initial_states=None, return_final_states=
     """K3: (S_in [b, c, h, P, N], final [b, h, P, N]) from local states (MR:152-157).
 
     Works on a copy: the input ``states`` is left unchanged.  ``split``
-    (torch.bfloat16 / torch.float16, f32 states only): S_in is stored as that
-    type's (hi, lo) pairs for ``chunk_scan(..., split=True)``.
+    (f32 states only): torch.bfloat16 / torch.float16 store S_in as that
+    type's (hi, lo) pairs for ``chunk_scan(..., split=True)``; "f16s" as f16
+    rows with a power-of-two scale per row for ``chunk_scan(..., split="f16s")``.
     """
     S = states.detach().clone(memory_format=torch.contiguous_format)
     final = (torch.empty((S.shape[0], S.shape[2], S.shape[3], S.shape[4]), dtype=torch.float32, device=S.device)
              if return_final_states else None)
-    state_passing_(S, chunk_decay, initial_states, final, split=split)
-    return S, final
+    scales = torch.empty(S.shape[:4], dtype=torch.float32, device=S.device) if split == "f16s" else None
+    state_passing_(S, chunk_decay, initial_states, final, split=split, scales=scales)
+    return (F16SStates(S, scales) if scales is not None else S), final
 
 
-def state_passing_(states, chunk_decay, initial_states=None, final_states=None, split=None):
+def state_passing_(states, chunk_decay, initial_states=None, final_states=None, split=None, scales=None):
     """K3 in place on a contiguous ``states`` buffer (local states in, S_in out);
-    ``final_states`` (optional, [b, h, P, N] float32) receives the last state."""
+    ``final_states`` (optional, [b, h, P, N] float32) receives the last state;
+    ``scales`` ([b, c, h, P] float32) the row scales when split="f16s"."""
     b, nc, h, P, N = states.shape
     dev = _device_check(states, chunk_decay, initial_states, final_states)
     if not states.is_contiguous():
@@ -353,9 +391,13 @@ def state_passing_(states, chunk_decay, initial_states=None, final_states=None, 
                                      or final_states.shape != (b, h, P, N)):
         raise ValueError("final_states must be a contiguous float32 [b, h, P, N] tensor")
     if split is not None and (states.dtype != torch.float32 or split not in _SPLIT_STATES):
-        raise ValueError("split storage needs float32 states and split=torch.bfloat16 or torch.float16")
+        raise ValueError('split storage needs float32 states and split=torch.bfloat16, torch.float16 or "f16s"')
     sd = _STATE_DTYPES[states.dtype] if split is None else _SPLIT_STATES[split]
-    _lib.check(_lib.load().ssd_state_passing(ctypes.byref(d), _ptr(states), sd,
+    if split == "f16s":
+        _expect("scales", scales, (b, nc, h, P), torch.float32)
+        if scales is None or not scales.is_contiguous() or scales.device != dev:
+            raise ValueError(f"f16s states need a contiguous float32 scales tensor {(b, nc, h, P)} on {dev}")
+    _lib.check(_lib.load().ssd_state_passing(ctypes.byref(d), _ptr(states), sd, _ptr(scales if split == "f16s" else None),
                                              _ptr(decay), _ptr(init), _ptr(final_states), _stream(dev)))
     return states
 
@@ -383,17 +425,18 @@ def chunk_state_passing(X, B, Acs, chunk_decay, dt=None, prep=None, initial_stat
     init = _f32_contig(initial_states)
     if split is not None:
         if split not in _SPLIT_STATES:
-            raise ValueError("split must be torch.bfloat16 or torch.float16")
+            raise ValueError('split must be torch.bfloat16, torch.float16 or "f16s"')
         sd, store = _SPLIT_STATES[split], torch.float32
     else:
         sd, store = _STATE_DTYPES[state_dtype], state_dtype
     states = torch.empty((b, L // Q, h, P, N), dtype=store, device=dev)
     final = torch.empty((b, h, P, N), dtype=torch.float32, device=dev) if return_final_states else None
+    scales = torch.empty((b, L // Q, h, P), dtype=torch.float32, device=dev) if split == "f16s" else None
     _lib.check(_lib.load().ssd_chunk_state_passing(
         ctypes.byref(d), _DTYPES[X.dtype], _ptr(X), _lib.strides(X), _ptr(Bm), _lib.strides(Bm),
         _ptr(dt), _lib.strides(dt) if dt is not None else None, _ptr(Acs), _ptr(decay), _ptr(prep), _ptr(init),
-        _ptr(states), sd, _ptr(final), _stream(dev)))
-    return states, final
+        _ptr(states), sd, _ptr(scales), _ptr(final), _stream(dev)))
+    return (F16SStates(states, scales) if scales is not None else states), final
 
 
 def _epilogue(X, D, z, dev):
@@ -423,15 +466,26 @@ def _epilogue(X, D, z, dev):
 
 def chunk_scan(X, B, C, Acs, states, dt=None, prep=None, split=False, D=None, z=None):
     """K4: Y [b, L, h, P] from the states entering each chunk (MR:139-145, 160-162).
-    ``prep``: chunk_prep(B, C, Q) or None.  ``split``: ``states`` holds
-    state_passing(..., split=X.dtype)'s (hi, lo) pairs.  ``D`` [h] and / or
+    ``prep``: chunk_prep(B, C, Q) or None.  ``split``: True when ``states``
+    holds state_passing(..., split=X.dtype)'s (hi, lo) pairs, "f16s" for
+    state_passing(..., split="f16s")'s scaled f16 rows.  ``D`` [h] and / or
     ``z`` (X's shape and dtype): the layer's skip and gate fused into the write,
     Y = (Y + D x) * silu(z) (MR:116-118)."""
     b, L, h, P = X.shape
     g, N = B.shape[2], B.shape[3]
     Q = Acs.shape[-1]
-    dev = _device_check(X, B, C, Acs, states, dt, prep)
+    scales = None
+    if isinstance(states, F16SStates):
+        if split not in (False, "f16s"):
+            raise ValueError('F16SStates are read with split="f16s"')
+        split, states, scales = "f16s", states.states, states.scales
+    elif split == "f16s":
+        raise ValueError('split="f16s" needs the F16SStates that state_passing(..., split="f16s") returns')
+    dev = _device_check(X, B, C, Acs, states, dt, prep, scales)
     d = _dims(b, L, h, P, N, g, Q)
+    if scales is not None:
+        _expect("scales", scales, (b, L // Q, h, P), torch.float32)
+        scales = scales.contiguous()
     if C.shape != B.shape or C.dtype != B.dtype:
         raise ValueError("B and C must have the same shape and dtype")
     _expect("Acs", Acs, (b, h, L // Q, Q))
@@ -441,8 +495,10 @@ def chunk_scan(X, B, C, Acs, states, dt=None, prep=None, split=False, D=None, z=
     _expect("states", states, (b, L // Q, h, P, N), torch.float32 if split else None)
     if not split and states.dtype not in _STATE_DTYPES:
         raise ValueError(f"unsupported state dtype {states.dtype}")
-    if split and X.dtype not in _SPLIT_STATES:
+    if split and X.dtype not in (torch.bfloat16, torch.float16):
         raise ValueError("split states need 16-bit inputs")
+    if split not in (False, True, "f16s"):
+        raise ValueError(f'split must be False, True or "f16s", got {split!r}')
     _check_prep(prep, d)
     X, Bm, Cm = _vec_operand(X.detach()), _vec_operand(B.detach()), _vec_operand(C.detach())
     Acs = _f32_contig(Acs)
@@ -455,7 +511,8 @@ def chunk_scan(X, B, C, Acs, states, dt=None, prep=None, split=False, D=None, z=
     _lib.check(_lib.load().ssd_chunk_scan(
         ctypes.byref(d), _DTYPES[X.dtype], _ptr(X), _lib.strides(X), _ptr(Bm), _lib.strides(Bm),
         _ptr(Cm), _lib.strides(Cm), _ptr(dt), _lib.strides(dt) if dt is not None else None,
-        _ptr(Acs), _ptr(S), _SPLIT_STATES[X.dtype] if split else _STATE_DTYPES[S.dtype], _ptr(Y),
+        _ptr(Acs), _ptr(S), (_SPLIT_STATES["f16s" if split == "f16s" else X.dtype] if split
+                             else _STATE_DTYPES[S.dtype]), _ptr(scales), _ptr(Y),
         _lib.strides(Y), _ptr(prep), ctypes.byref(epi) if epi is not None else None, _stream(dev)))
     return Y
 
