@@ -162,9 +162,11 @@ int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, float* s
  * state entering each chunk, [b, c, h, P, N]) in state_dtype, exactly as
  * ssd_chunk_state (f32 local states for the SPLIT formats, else state_dtype)
  * followed by ssd_state_passing would leave it.  For a SPLIT state_dtype of
- * the inputs' type with prep (chunk 256), the two stages run as one launch
- * wherever that is faster on the device: each (b, h) chain of chunks keeps
- * its running state in registers and the local states are never stored.
+ * the inputs' type with prep (chunk 256), and for f32 inputs with f32 states
+ * at chunk 64 / 128 and dstate 64 / 128 (chunk x dstate <= 8192), the two
+ * stages run as one launch (for SPLIT, wherever that is faster on the
+ * device): each (b, h) chain of chunks keeps its running state in registers
+ * and the local states are never stored.
  * Replaces MR:144-157 (X*dt, decay_to_end, block_state, the state loop).
  * a_cumsum, chunk_decay: ssd_chunk_cumsum's outputs; prep as for
  * ssd_chunk_state; initial_states / final_states as for ssd_state_passing. */

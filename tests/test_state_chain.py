@@ -1,4 +1,5 @@
-"""The chunk-256 forward runs chunk_state and state_passing as one launch
+"""The chunk-256 forward (and the f32 forward at chunk 64 / 128, at the end
+of this file) runs chunk_state and state_passing as one launch
 (each workgroup walks one (batch, head) chain of chunks with the running
 state in registers, workloads/mamba/model_ref.py:144-157) when the chains
 keep every CU about equally busy: at least 3/4 of the busiest CU's chains on
@@ -148,3 +149,54 @@ def test_chunk_state_passing_entry_point(b, h, L, split):
     assert torch.equal(final, f_ref)
     fmt = "f16s" if split == "f16s" else "split"
     assert torch.equal(handover_bytes(S_in, fmt), handover_bytes(S_ref, fmt))
+
+
+# ---------------------------------------------------------------------------
+# f32 inputs and states (chunk 64 / 128): K2 + K3 always run as one launch
+# where chunk x d_state <= 8192
+# ---------------------------------------------------------------------------
+
+F32_SHAPES = [
+    # (b, L, h, N, g, Q): 192 chains of 32 chunks (C2-like), many short chains
+    # with groups (C5-like), one chunk per chain, chunk 128 x d_state 128
+    # (no one-launch form: chunk_state then state_passing)
+    (2, 2048, 24, 128, 1, 64),
+    (8, 512, 64, 64, 8, 128),
+    (3, 128, 20, 64, 4, 128),
+    (2, 640, 6, 128, 3, 64),
+    (1, 512, 4, 128, 2, 128),
+]
+
+
+@pytest.mark.parametrize("b,L,h,N,g,Q", F32_SHAPES)
+@pytest.mark.parametrize("with_dt,with_init", [(True, True), (False, False), (False, True)])
+def test_f32_chain_entry_point(b, L, h, N, g, Q, with_dt, with_init):
+    """ssd_chunk_state_passing on f32 inputs and states against chunk_state
+    then state_passing: S_in and the final state bit for bit."""
+    print("CASE f32 chain", b, L, h, N, g, Q, with_dt, with_init, flush=True)
+    X, A, B, C, dt, init = case(torch.float32, b, L, h, 64, N, g, seed=L + h + N)
+    dt = dt if with_dt else None
+    init = init if with_init else None
+    Acs, decay = S.chunk_cumsum(A, Q)
+    S_in, final = S.chunk_state_passing(X, B, Acs, decay, dt=dt, initial_states=init)
+    st = S.chunk_state(X, B, Acs, dt=dt)
+    S_ref, f_ref = S.state_passing(st, decay, initial_states=init)
+    torch.cuda.synchronize()
+    assert torch.equal(final, f_ref)
+    assert torch.equal(S_in, S_ref)
+
+
+@pytest.mark.parametrize("b,L,h,N,g,Q", F32_SHAPES[:3])
+def test_f32_forward_equals_kernels_one_by_one(b, L, h, N, g, Q):
+    """ssd_forward on f32 inputs (the one-launch state chain) against K1, K2,
+    K3 and K4 through their own entry points: Y and the final state bit for bit."""
+    print("CASE f32 forward", b, L, h, N, g, Q, flush=True)
+    X, A, B, C, dt, init = case(torch.float32, b, L, h, 64, N, g, seed=3 * L + h)
+    Y, final = S.ssd_forward(X, A, B, C, Q, dt=dt, initial_states=init, return_final_states=True)
+    Acs, decay = S.chunk_cumsum(A, Q)
+    st = S.chunk_state(X, B, Acs, dt=dt)
+    S_in, fk = S.state_passing(st, decay, initial_states=init)
+    Yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dt)
+    torch.cuda.synchronize()
+    assert torch.equal(final, fk)
+    assert torch.equal(Y, Yk)

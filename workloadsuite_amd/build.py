@@ -27,9 +27,11 @@ SOURCES = [
     "ssd_chunk_prep.hip",
     "ssd_chunk_state.hip",
     "ssd_chunk_state_q256.hip",
+    "ssd_chunk_state_f32.hip",
     "ssd_state_passing.hip",
     "ssd_chunk_scan.hip",
     "ssd_chunk_scan_q256.hip",
+    "ssd_chunk_scan_f32.hip",
     "ssd_layer_prep.hip",
     "ssd_decode.hip",
     "ssd_noalloc.hip",

@@ -1,0 +1,367 @@
+// K2 -- chunk_state for f32 inputs and f32 states at chunk 64 / 128 and
+// d_state 64 / 128 (the Mamba-2-130M shape and the grouped short-sequence
+// shape).  Same result as the generic kernel in ssd_chunk_state.hip
+// (workloads/mamba/model_ref.py:144, 148-149):
+//   S[p, n] = sum_l (w[l] x[l, p]) B[l, n],   w[l] = exp(Acs[Q-1] - Acs[l]) dt[l]
+// stored as states[b, c, h, p, n].
+//
+// B does not depend on the head (MR:97-99 repeats it over the heads of a
+// group), so one workgroup takes one (b, c, group) -- or a slice of its heads
+// when there are few groups -- and keeps the B operand of its output tiles in
+// registers for all of them; per head only x (and Acs, dt) move, copied
+// global -> LDS one head ahead (global_load_lds, rows XOR-swizzled by 16-byte
+// piece so the column reads of the A operand are free of bank conflicts).
+// The weight w[l] is applied in f32 as the A operand is read: no rounding
+// beyond f32's.
+//
+// Work decomposition: 8 waves; wave w owns p tiles 2 (w % 2), 2 (w % 2) + 1
+// and n tiles [(w / 2) N / 64, (w / 2 + 1) N / 64).  K index slot (g, j) of
+// K step ks is token l = 32 ks + 16 (j / 4) + 4 g + j % 4 in both operands.
+#include "ssd_device.h"
+#include "ssd_launch.h"
+#include "../../include/ssd.h"
+
+namespace ssd {
+
+namespace {
+
+constexpr int kP = 64;
+constexpr int kNW = 8;
+constexpr int kThreads = 64 * kNW;
+
+// float offset of x / B element (l, col) in a staged block of rows of `cols`
+// floats: 16-byte piece col / 4 of row l sits at piece (col / 4) ^ 4 ((l >> 2) & 3)
+__device__ __forceinline__ int swz_off(int l, int col, int cols) {
+  return l * cols + 4 * ((col >> 2) ^ (4 * ((l >> 2) & 3))) + (col & 3);
+}
+
+// w[l] = exp(Acs[Q-1] - Acs[l]) dt[l] from Acs[l], log2(e) Acs[Q-1] and dt[l]
+// (exp2 of a non-positive argument for decaying chunks; results below f32's
+// normal range flush to 0)
+__device__ __forceinline__ float chunk_weight(float acs_l, float last_log2, float dt_l) {
+  return __builtin_amdgcn_exp2f(__builtin_fmaf(acs_l, -kLog2e, last_log2)) * dt_l;
+}
+
+template <int NK, int RT, bool HAS_DT>
+__global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArgs p, int hs, int slices) {
+  constexpr int Q = 64 * RT;
+  constexpr int N = 32 * NK;
+  constexpr int KS = Q / 32;             // K steps of 32 tokens
+  constexpr int NTW = N / 64;            // n tiles per wave
+  constexpr int XPW = Q * kP / 256 / kNW;  // x copies (1 KB) per wave and head
+  constexpr int BPW = Q * N / 256 / kNW;   // B copies per wave
+  // x buffers 0 and 1, then room for B (staged once, over buffer 1)
+  constexpr int LDS_F = 2 * Q * kP > Q * kP + Q * N ? 2 * Q * kP : Q * kP + Q * N;
+  __shared__ __attribute__((aligned(1024))) float lds[LDS_F];
+  __shared__ __attribute__((aligned(16))) float al[2][Q];
+  __shared__ __attribute__((aligned(16))) float dl[HAS_DT ? 2 : 1][HAS_DT ? Q : 4];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, i = lane & 15;
+  const int pp = wave & 1, nt0 = (wave >> 1) * NTW;
+
+  const int u = blockIdx.x;
+  const int slice = u % slices, bcg = u / slices;
+  const int grp = bcg % p.ngroups, bc = bcg / p.ngroups;
+  const int c = bc % p.nchunks, b = bc / p.nchunks;
+  const int hpg = p.nheads / p.ngroups;
+  const int h0 = grp * hpg + slice * hs;
+  const int h1 = min(h0 + hs, (grp + 1) * hpg);
+  if (h0 >= h1) return;  // the whole workgroup, before any barrier
+  const int64_t l0 = (int64_t)c * Q;
+
+  const float* xg0 = reinterpret_cast<const float*>(p.x) + b * p.sxb + l0 * p.sxl;
+  const float* bg = reinterpret_cast<const float*>(p.bm) + b * p.sbb + l0 * p.sbl + grp * p.sbg;
+  const uint32_t lds_base = lds_offset(&lds[0]);
+  const uint32_t al_lds = lds_offset(&al[0][0]), dl_lds = lds_offset(&dl[0][0]);
+
+  // rows of `cols` floats, 1 KB copies: copy blk moves rows blk * 1024 / (4 cols) ...
+  auto issue_rows = [&](const float* src, int64_t ld, int cols, int blk, uint32_t dst) __attribute__((always_inline)) {
+    const int ppr = cols / 4, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ (4 * ((r >> 2) & 3));
+    dma16_at(src + r * ld + 4 * pc, dst + (uint32_t)(blk * 1024));
+  };
+  auto issue_head = [&](int h, int bf) __attribute__((always_inline)) {
+    const float* xg = xg0 + h * p.sxh;
+#pragma unroll
+    for (int m = 0; m < XPW; ++m) issue_rows(xg, p.sxl, kP, wave + kNW * m, lds_base + (uint32_t)(bf * Q * kP * 4));
+    if (wave == kNW - 1 && lane < Q / 4) {
+      const float* ag = p.acs + (((int64_t)b * p.nheads + h) * p.nchunks + c) * Q;
+      dma16_at(ag + 4 * lane, al_lds + (uint32_t)(bf * Q * 4));
+    }
+    if constexpr (HAS_DT) {
+      if (wave >= kNW - 1 - Q / 64 && wave < kNW - 1) {
+        const int part = wave - (kNW - 1 - Q / 64);
+        const float* dg = p.dt + b * p.sdb + h * p.sdh;
+        dma4_at(dg + (l0 + 64 * part + lane) * p.sdl, dl_lds + (uint32_t)((bf * Q + 64 * part) * 4));
+      }
+    }
+  };
+
+  // ---- per slice: B operands of this wave's n tiles, via LDS ----
+  issue_head(h0, 0);
+#pragma unroll
+  for (int m = 0; m < BPW; ++m) issue_rows(bg, p.sbl, N, wave + kNW * m, lds_base + (uint32_t)(Q * kP * 4));
+  dma_wait();
+  __syncthreads();
+  frag8<float> bfr[NTW][KS];
+  {
+    const float* bl = lds + Q * kP;
+#pragma unroll
+    for (int n = 0; n < NTW; ++n)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          bfr[n][ks][j] = bl[swz_off(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)];
+  }
+  __syncthreads();  // B's LDS is x buffer 1 from here on
+
+  f32x4 acc[2][NTW];
+  int hprev = -1;
+  // states[b, c, h, p, n] of head hs_ from acc (rows p = 16 pt + 4 g + jj, columns n = 16 nt + i)
+  auto store_states = [&](int hst) __attribute__((always_inline)) {
+    float* sg = reinterpret_cast<float*>(p.states) + (((int64_t)b * p.nchunks + c) * p.nheads + hst) * (kP * N);
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int n = 0; n < NTW; ++n)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          sg[(16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] = acc[a][n][jj];
+  };
+
+  for (int h = h0; h < h1; ++h) {
+    const int bf = (h - h0) & 1;
+    // the previous head's states, then the next head's copies: the wait at
+    // the end of this head covers both
+    if (hprev >= 0) store_states(hprev);
+    if (h + 1 < h1) issue_head(h + 1, bf ^ 1);
+    hprev = h;
+    const float* xb = lds + bf * Q * kP;
+    const float* ab = al[bf];
+    const float last = ab[Q - 1] * kLog2e;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int n = 0; n < NTW; ++n) acc[a][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      // w[l] of this lane's 8 tokens
+      float w[8];
+#pragma unroll
+      for (int st = 0; st < 2; ++st) {
+        const int l = 32 * ks + 16 * st + 4 * g;
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(ab + l);
+        f32x4 d4 = f32x4{1.f, 1.f, 1.f, 1.f};
+        if constexpr (HAS_DT) d4 = *reinterpret_cast<const f32x4*>(&dl[bf][l]);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) w[4 * st + jj] = chunk_weight(a4[jj], last, d4[jj]);
+      }
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int col = 16 * (2 * pp + a) + i;
+        frag8<float> xf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xf[j] = xb[swz_off(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)] * w[j];
+#pragma unroll
+        for (int n = 0; n < NTW; ++n) acc[a][n] = mma(xf, bfr[n][ks], acc[a][n]);
+      }
+    }
+    dma_wait();
+    __syncthreads();
+  }
+  store_states(hprev);
+}
+
+// K2 + K3 in one launch for f32 inputs and f32 states: one workgroup per
+// (b, h) chain walks the chunks in order, computes each chunk's local state
+// exactly as chunk_state_f32_kernel does (same operands, same MFMA and FMA
+// order), and advances the running state held in registers,
+// h <- h * decay[c] + local (workloads/mamba/model_ref.py:152-157) -- the
+// same f32 FMA per element and chunk as state_passing -- after storing the
+// state entering the chunk, S_in[c], in the f32 states layout.  The local
+// states never reach memory.  x and B of the next chunk are copied
+// global -> LDS while the current chunk computes; the chains of one group's
+// heads run on one XCD and share B through its L2.
+template <int NK, int RT, bool HAS_DT>
+__global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkStateArgs p, StatePassingArgs sp) {
+  constexpr int Q = 64 * RT;
+  constexpr int N = 32 * NK;
+  constexpr int KS = Q / 32;
+  constexpr int NTW = N / 64;
+  constexpr int XPW = Q * kP / 256 / kNW;
+  constexpr int BPW = Q * N / 256 / kNW;
+  __shared__ __attribute__((aligned(1024))) float xs[2][Q * kP];
+  __shared__ __attribute__((aligned(1024))) float bs[2][Q * N];
+  __shared__ __attribute__((aligned(16))) float al[2][Q];
+  __shared__ __attribute__((aligned(16))) float dl[HAS_DT ? 2 : 1][HAS_DT ? Q : 4];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 4, i = lane & 15;
+  const int pp = wave & 1, nt0 = (wave >> 1) * NTW;
+  // consecutive chains (the heads of a group) on one XCD
+  const int bh = __builtin_amdgcn_readfirstlane(xcd_remap(blockIdx.x, gridDim.x));
+  const int h = bh % p.nheads, b = bh / p.nheads;
+  const int grp = h / (p.nheads / p.ngroups);
+
+  const float* xg = reinterpret_cast<const float*>(p.x) + b * p.sxb + h * p.sxh;
+  const float* bg = reinterpret_cast<const float*>(p.bm) + b * p.sbb + grp * p.sbg;
+  const float* dg = HAS_DT ? p.dt + b * p.sdb + h * p.sdh : nullptr;
+  const uint32_t xs_lds = lds_offset(&xs[0][0]), bs_lds = lds_offset(&bs[0][0]);
+  const uint32_t al_lds = lds_offset(&al[0][0]), dl_lds = lds_offset(&dl[0][0]);
+  auto issue_rows = [&](const float* src, int64_t ld, int cols, int blk, uint32_t dst) __attribute__((always_inline)) {
+    const int ppr = cols / 4, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ (4 * ((r >> 2) & 3));
+    dma16_at(src + r * ld + 4 * pc, dst + (uint32_t)(blk * 1024));
+  };
+  auto issue_chunk = [&](int c, int bf) __attribute__((always_inline)) {
+    const int64_t l0 = (int64_t)c * Q;
+#pragma unroll
+    for (int m = 0; m < XPW; ++m) issue_rows(xg + l0 * p.sxl, p.sxl, kP, wave + kNW * m, xs_lds + (uint32_t)(bf * Q * kP * 4));
+#pragma unroll
+    for (int m = 0; m < BPW; ++m) issue_rows(bg + l0 * p.sbl, p.sbl, N, wave + kNW * m, bs_lds + (uint32_t)(bf * Q * N * 4));
+    if (wave == kNW - 1 && lane < Q / 4) {
+      const float* ag = p.acs + ((int64_t)bh * p.nchunks + c) * Q;
+      dma16_at(ag + 4 * lane, al_lds + (uint32_t)(bf * Q * 4));
+    }
+    if constexpr (HAS_DT) {
+      if (wave >= kNW - 1 - Q / 64 && wave < kNW - 1) {
+        const int part = wave - (kNW - 1 - Q / 64);
+        dma4_at(dg + (l0 + 64 * part + lane) * p.sdl, dl_lds + (uint32_t)((bf * Q + 64 * part) * 4));
+      }
+    }
+  };
+
+  // running state: S_in of the current chunk, rows p = 16 pt + 4 g + jj, columns n = 16 nt + i
+  const int64_t PN = (int64_t)kP * N;
+  f32x4 st[2][NTW];
+#pragma unroll
+  for (int a = 0; a < 2; ++a)
+#pragma unroll
+    for (int n = 0; n < NTW; ++n)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        st[a][n][jj] = sp.init ? sp.init[bh * PN + (16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] : 0.f;
+  issue_chunk(0, 0);
+  dma_wait();
+  __syncthreads();
+
+  for (int c = 0; c < p.nchunks; ++c) {
+    const int bf = c & 1;
+    if (c + 1 < p.nchunks) issue_chunk(c + 1, bf ^ 1);
+    const float dec = sp.decay[(int64_t)bh * p.nchunks + c];
+    const float* xb = xs[bf];
+    const float* bl = bs[bf];
+    const float* ab = al[bf];
+    const float last = ab[Q - 1] * kLog2e;
+    f32x4 acc[2][NTW];
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int n = 0; n < NTW; ++n) acc[a][n] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      float w[8];
+#pragma unroll
+      for (int s2 = 0; s2 < 2; ++s2) {
+        const int l = 32 * ks + 16 * s2 + 4 * g;
+        const f32x4 a4 = *reinterpret_cast<const f32x4*>(ab + l);
+        f32x4 d4 = f32x4{1.f, 1.f, 1.f, 1.f};
+        if constexpr (HAS_DT) d4 = *reinterpret_cast<const f32x4*>(&dl[bf][l]);
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) w[4 * s2 + jj] = chunk_weight(a4[jj], last, d4[jj]);
+      }
+      frag8<float> bfr[NTW];
+#pragma unroll
+      for (int n = 0; n < NTW; ++n)
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+          bfr[n][j] = bl[swz_off(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)];
+#pragma unroll
+      for (int a = 0; a < 2; ++a) {
+        const int col = 16 * (2 * pp + a) + i;
+        frag8<float> xf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xf[j] = xb[swz_off(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)] * w[j];
+#pragma unroll
+        for (int n = 0; n < NTW; ++n) acc[a][n] = mma(xf, bfr[n], acc[a][n]);
+      }
+    }
+    // S_in[c], then the recurrence (state_passing's f32 FMA)
+    float* sg = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * PN;
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int n = 0; n < NTW; ++n) {
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) sg[(16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] = st[a][n][jj];
+        st[a][n] = st[a][n] * dec + acc[a][n];
+      }
+    dma_wait();
+    __syncthreads();
+  }
+  if (sp.final_state) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int n = 0; n < NTW; ++n)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj)
+          sp.final_state[bh * PN + (16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] = st[a][n][jj];
+  }
+}
+
+template <int NK, int RT>
+hipError_t launch_chain_qn(const ChunkStateArgs& a, const StatePassingArgs& sp, hipStream_t stream) {
+  const int64_t chains = (int64_t)a.batch * a.nheads;
+  if (chains > INT32_MAX) return hipErrorInvalidValue;
+  auto kern = a.dt ? chunk_state_chain_f32_kernel<NK, RT, true> : chunk_state_chain_f32_kernel<NK, RT, false>;
+  kern<<<dim3((unsigned)chains), dim3(kThreads), 0, stream>>>(a, sp);
+  return hipGetLastError();
+}
+
+template <int NK, int RT>
+hipError_t launch_qn(const ChunkStateArgs& a, hipStream_t stream) {
+  const int hpg = a.nheads / a.ngroups;
+  const int64_t bcg = (int64_t)a.batch * a.nchunks * a.ngroups;
+  // slices of a group's heads: enough workgroups for every CU, B loaded as
+  // few times as that allows
+  const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
+  int slices = (int)((cus + bcg - 1) / bcg);
+  if (slices > hpg) slices = hpg;
+  if (slices < 1) slices = 1;
+  const int hs = (hpg + slices - 1) / slices;
+  slices = (hpg + hs - 1) / hs;
+  const int64_t grid = bcg * slices;
+  if (grid > INT32_MAX) return hipErrorInvalidValue;
+  auto kern = a.dt ? chunk_state_f32_kernel<NK, RT, true> : chunk_state_f32_kernel<NK, RT, false>;
+  kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(a, hs, slices);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+bool chunk_state_f32_supported(const ChunkStateArgs& a, int dtype, int state_dtype) {
+  return dtype == SSD_DTYPE_F32 && state_dtype == SSD_DTYPE_F32 && (a.chunk == 64 || a.chunk == 128) &&
+         (a.dstate == 64 || a.dstate == 128);
+}
+
+bool chunk_state_chain_f32_supported(const ChunkStateArgs& a, int dtype, const StatePassingArgs& sp) {
+  // two chunks of x and B in LDS: chunk x d_state up to 8192
+  return chunk_state_f32_supported(a, dtype, SSD_DTYPE_F32) && a.chunk * a.dstate <= 8192 && !sp.split_dtype &&
+         !sp.f16s && sp.bh_begin == 0 && (sp.bh_count == 0 || sp.bh_count == a.batch * a.nheads);
+}
+
+hipError_t launch_chunk_state_chain_f32(const ChunkStateArgs& a, const StatePassingArgs& sp, hipStream_t stream) {
+  if (a.chunk == 64) return a.dstate == 64 ? launch_chain_qn<2, 1>(a, sp, stream) : launch_chain_qn<4, 1>(a, sp, stream);
+  if (a.chunk == 128 && a.dstate == 64) return launch_chain_qn<2, 2>(a, sp, stream);
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_chunk_state_f32(const ChunkStateArgs& a, hipStream_t stream) {
+  if (a.chunk == 64) return a.dstate == 64 ? launch_qn<2, 1>(a, stream) : launch_qn<4, 1>(a, stream);
+  return a.dstate == 64 ? launch_qn<2, 2>(a, stream) : launch_qn<4, 2>(a, stream);
+}
+
+}  // namespace ssd
