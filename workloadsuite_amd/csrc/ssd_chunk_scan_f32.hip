@@ -13,8 +13,9 @@
 // d_state 128) to 50% (chunk 128, d_state 64) of a head's MFMA work.
 //
 // Work decomposition: 8 waves; wave w owns row tiles t (rows 16 t .. 16 t +
-// 15 of the chunk) -- t = w % 4 at chunk 64, t = w % 4 and 7 - w % 4 at chunk
-// 128, which gives every wave the same number of diagonal blocks -- and p
+// 15 of the chunk) -- at chunk 64 t = w % 4 for w < 4 and 3 - w % 4 above
+// (so the two waves of each SIMD together hold three diagonal blocks), at
+// chunk 128 t = w % 4 and 7 - w % 4 (five blocks for every wave) -- and p
 // tiles 2 (w / 4) and 2 (w / 4) + 1.  Per wave and for the whole slice of
 // heads: C fragments of its rows (the A operand of C.S^T and the B operand of
 // C.B^T) and the raw C.B^T sub-tiles [s][l] of its rows in the D layout (4
@@ -52,7 +53,9 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_f32_kernel(ChunkScanArgs 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 4, i = lane & 15;
-  const int rg = wave & 3, ph = wave >> 2;
+  // the two waves of SIMD s (w = s, s + 4) take row groups s and 3 - s, so
+  // every SIMD holds the same number of diagonal blocks at chunk 64
+  const int ph = wave >> 2, rg = RT == 1 && ph ? 3 - (wave & 3) : wave & 3;
   int trow[RT];
   trow[0] = rg;
   if constexpr (RT == 2) trow[1] = 7 - rg;
