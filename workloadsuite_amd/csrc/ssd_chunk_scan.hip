@@ -41,8 +41,15 @@ namespace {
 constexpr int kP = 64;
 constexpr int kSB = 32;  // tokens s per diagonal step
 
+// f32 at d_state 128 with chunk 128 / 256 holds 64 / 128 VGPRs of C
+// fragments alone: one workgroup per CU (one wave per SIMD, whose full
+// register file the compiler may then use) instead of two, and no scratch.
+template <typename T, int NK, int RT> constexpr int scan_blocks_per_cu() {
+  return sizeof(T) == 4 && NK * RT >= 8 ? 1 : 2;
+}
+
 template <typename T, typename S, int NK, int RT>
-__global__ __launch_bounds__(256, 2) void chunk_scan_kernel(ChunkScanArgs p) {
+__global__ __launch_bounds__(256, (scan_blocks_per_cu<T, NK, RT>())) void chunk_scan_kernel(ChunkScanArgs p) {
   constexpr int Q = 64 * RT;
   constexpr int NP = 32 * NK;                 // dstate padded to the MFMA K step
   constexpr int PAD = 16 / sizeof(T);

@@ -456,14 +456,15 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     if constexpr (F16S) {
       // rows p of the off-diagonal tiles carry their S_in row scale, columns
       // l the C row scale and exp(Acs[l])
-      f32x4 sc[4];
+      // (one column tile's scales at a time: fewer live registers)
+      float e[2];
 #pragma unroll
-      for (int pt = 0; pt < 4; ++pt) sc[pt] = *reinterpret_cast<const f32x4*>(&scl[b][16 * pt + 4 * g]);
+      for (int s2 = 0; s2 < 2; ++s2) e[s2] = __builtin_amdgcn_exp2f(al[s2]) * cs[s2];
 #pragma unroll
-      for (int s2 = 0; s2 < 2; ++s2) {
-        const float e = __builtin_amdgcn_exp2f(al[s2]) * cs[s2];
+      for (int pt = 0; pt < 4; ++pt) {
+        const f32x4 sc = *reinterpret_cast<const f32x4*>(&scl[b][16 * pt + 4 * g]);
 #pragma unroll
-        for (int pt = 0; pt < 4; ++pt) acc[s2][pt] *= sc[pt] * e;
+        for (int s2 = 0; s2 < 2; ++s2) acc[s2][pt] *= sc * e[s2];
       }
     } else {
 #pragma unroll
