@@ -1,0 +1,481 @@
+"""CPU-side bounds check of the kernels' per-lane global and LDS address
+arithmetic at the C1-C5 and R0 shapes (no GPU).
+
+The persistent and DMA-staged kernels form every global address from an item
+base (batch, chunk, head or group) plus a per-lane offset (wave, lane, copy
+part, loop step), and the global -> LDS copies (global_load_lds) write 16 or
+4 bytes per lane at a wave-uniform LDS base.  A wrong lane formula would read
+or write outside a tensor or an LDS buffer, which on the GPU is a memory
+fault, not a test failure.  Each check below restates one kernel's formulas
+in numpy, evaluates them over every workgroup, wave, lane and loop step the
+launch runs at a shape, and asserts that every element touched lies inside
+its tensor (as an index in range in each dimension, which also holds for
+strided views) and every LDS byte inside its buffer.
+
+Kernels per shape: C3, C4 and the R0 layer span (16-bit, chunk 256) run
+chunk_prep, the persistent chunk_state / chunk_scan and the state chain; C2
+and C5 (f32, chunk 64 / 128) the f32 chunk_scan, chunk_state and chain; every
+shape runs state_passing.  C1 (d_state 16) and R0's core at chunk 64 run only
+the generic chunk_state / chunk_scan besides, whose staging loops bound every
+row and column by the shape explicitly (ssd_device.h stage_rows /
+stage_transposed) instead of by lane arithmetic.
+
+The restatements are pinned to the source: each check first asserts that
+the lines it restates still read as below in the kernel file
+(whitespace-normalised), so a change to a kernel's address arithmetic fails
+here until the check is updated with it.
+"""
+
+import pathlib
+import re
+
+import numpy as np
+import pytest
+
+SRC = pathlib.Path(__file__).resolve().parent.parent / "workloadsuite_amd" / "csrc"
+CUS = 256  # MI355X
+
+# (batch, seqlen, nheads, headdim, dstate, chunk, ngroups, 16-bit inputs)
+SHAPES = {
+    "C1": (16, 128, 8, 64, 16, 64, 8, False),
+    "C2": (8, 2048, 24, 64, 128, 64, 1, False),
+    "C3": (4, 4096, 80, 64, 128, 256, 1, True),
+    "C4": (1, 65536, 80, 64, 128, 256, 1, True),
+    "C5": (64, 512, 64, 64, 64, 128, 8, False),
+    "R0": (8, 2048, 128, 64, 128, 64, 8, True),        # the module's core at chunk 64
+    "R0-layer": (8, 2048, 128, 64, 128, 256, 8, True),  # the layer span at chunk 256
+}
+
+_src_cache = {}
+
+
+def pin(fname, *snippets):
+    """The kernel file still contains each restated line."""
+    if fname not in _src_cache:
+        _src_cache[fname] = re.sub(r"\s+", " ", (SRC / fname).read_text())
+    text = _src_cache[fname]
+    for s in snippets:
+        assert re.sub(r"\s+", " ", s) in text, f"{fname} no longer contains: {s}"
+
+
+def inside(name, idx, lo, hi):
+    """lo <= idx < hi for every element (idx: array of indices touched)."""
+    idx = np.asarray(idx)
+    assert idx.size > 0, name
+    mn, mx = int(idx.min()), int(idx.max())
+    assert lo <= mn and mx < hi, f"{name}: touches [{mn}, {mx}], allowed [{lo}, {hi})"
+
+
+def lanes():
+    """(wave, lane) grids of an 8-wave workgroup, shapes [8, 1] and [1, 64]."""
+    return np.arange(8)[:, None], np.arange(64)[None, :]
+
+
+def xcd_remap(bid, n):
+    """ssd_device.h: xcd_remap (8 XCDs, workgroups dispatched round-robin)."""
+    per, rem = n // 8, n % 8
+    x, k = bid % 8, bid // 8
+    start = np.where(x < rem, x * (per + 1), rem * (per + 1) + (x - rem) * per)
+    return start + k
+
+
+def test_xcd_remap_is_a_permutation():
+    pin("ssd_device.h",
+        "const int per = nblocks / kXcds, rem = nblocks % kXcds;",
+        "const int x = bid % kXcds, k = bid / kXcds;",
+        "const int start = x < rem ? x * (per + 1) : rem * (per + 1) + (x - rem) * per;",
+        "return start + k;")
+    for n in list(range(1, 300)) + [1024, 2047, 2048, 20480, 65536 + 3]:
+        m = xcd_remap(np.arange(n), n)
+        assert np.array_equal(np.sort(m), np.arange(n)), n
+
+
+@pytest.mark.parametrize("nitems", [1, 7, 320, 5120, 20480, 8192, 16384])
+def test_persistent_item_ranges_partition_the_items(nitems):
+    """it0 = lb * n / grid, it1 = (lb + 1) * n / grid over every grid size a
+    persistent launch can take (one up to two workgroups per CU, capped by the
+    item count): the ranges lie in [0, n) and cover it exactly once."""
+    pin("ssd_chunk_scan_q256.hip",
+        "const int it0 = (int)((int64_t)lb * nitems / gridDim.x);",
+        "const int it1 = (int)((int64_t)(lb + 1) * nitems / gridDim.x);")
+    for grid in sorted({min(nitems, g) for g in (1, 3, CUS, 2 * CUS, 3 * CUS)}):
+        lb = xcd_remap(np.arange(grid), grid)
+        it0, it1 = lb * nitems // grid, (lb + 1) * nitems // grid
+        inside("it0", it0, 0, nitems)
+        inside("it1", it1, 1, nitems + 1)
+        cover = np.zeros(nitems, np.int64)
+        for a, b in zip(it0, it1):
+            cover[a:b] += 1
+        assert (cover == 1).all()
+
+
+def items(B, L, H, Q):
+    """item_of(it) for every item: (b, c, h) arrays, heads fastest."""
+    nc = L // Q
+    it = np.arange(B * nc * H)
+    h = it % H
+    bc = it // H
+    return bc // nc, bc % nc, h
+
+
+# ---------------------------------------------------------------------------
+# chunk-256 persistent chunk_scan (ssd_chunk_scan_q256.hip)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["C3", "C4", "R0-layer"])
+@pytest.mark.parametrize("fmt", ["f16s", "split", "bf16"])
+def test_chunk_scan_q256_addresses(name, fmt):
+    B, L, H, P, N, Q, G, _ = SHAPES[name]
+    assert Q == 256 and P == 64
+    pin("ssd_chunk_scan_q256.hip",
+        "const int64_t xcopy = (int64_t)(lane >> 3) * p.sxl + 8 * ((lane & 7) ^ (lane >> 3));",
+        "const int blk = wave + kNW * part;",
+        "dma16_at(xg + (int64_t)(8 * blk) * p.sxl, xr_lds + (uint32_t)(b * kQ * kP * (int)sizeof(T) + blk * 1024));",
+        "const int scopy = (lane / PPR) * GRS + ((lane % PPR) ^ ssw(wave * RPD + lane / PPR)) * (16 / (int)sizeof(SE));",
+        "const int d = wave + kNW * part;",
+        "dma16_at(sg + d * RPD * GRS, sr_lds + (uint32_t)(b * kP * RB + d * 1024));",
+        "if (part == 1 && wave == 0) dma4_at(p.sscale + item * kP + lane, scl_lds + (uint32_t)(b * kP * 4));",
+        "dma16_at(ag + 4 * lane, ar_lds + (uint32_t)(wave * kQ * 4));",
+        "dma4_at(dg + (l0 + 64 * wave + lane) * p.sdl, dr_lds + (uint32_t)(b * kQ * 4 + 256 * wave));",
+        "const int ycol = 8 * (g >> 1) + 16 * (g & 1);",
+        "T* yrow = yg + (int64_t)(16 * (s2 ? tb : ta) + i) * p.syl + ycol;",
+        "*reinterpret_cast<u32x4*>(yrow + 32 * pp) = u32x4{w0[0], w1[0], w0[1], w1[1]};",
+        "store8<T>(yrow + 32 * pp, __builtin_convertvector(v, frag8<T>));",
+        "const int ta = wave, tb = kNT - 1 - wave;",
+        "cf[0][kc] = load8<T>(cg + (int64_t)(16 * ta + i) * p.scl + 32 * kc + 8 * g);",
+        "const int64_t wbase = (((int64_t)r.b * p.nchunks + r.c) * p.ngroups + r.grp) * kNW + wave;",
+        "const f32x4* cb = reinterpret_cast<const f32x4*>(p.cbf) + wbase * (kNPair * 2 * 64) + lane_o;",
+        "cbc[k].set(st, cb[(k * 2 + st) * 64]);",
+        "const frag8<T>* cb = reinterpret_cast<const frag8<T>*>(p.cbf) + wbase * (kNPair * 64) + lane_o;",
+        "zv[s2][pp] = load8<T>(zg + (int64_t)(16 * (s2 ? tb : ta) + i) * p.szl + 32 * pp);")
+    wave, lane = lanes()
+    g, i = lane >> 4, lane & 15
+    parts = np.arange(4)[:, None, None]
+    b, c, h = items(B, L, H, Q)
+    nc = L // Q
+    inside("item b", b, 0, B)
+    inside("item c", c, 0, nc)
+    inside("item h", h, 0, H)
+    # x copy: 8 elements of row l0 + 8 blk + lane / 8 from column 8 ((lane % 8) ^ (lane / 8))
+    blk = wave + 8 * parts
+    inside("x rows in the chunk", 8 * blk + (lane >> 3), 0, Q)
+    xcol = 8 * ((lane & 7) ^ (lane >> 3))
+    inside("x columns", np.concatenate([xcol, xcol + 7], None), 0, P)
+    inside("x LDS (2 buffers of Q x P x 2 bytes)", 1 * Q * P * 2 + blk * 1024 + 16 * lane + 15, 0, 2 * Q * P * 2)
+    # S_in copy (states [b, c, h, P, N] in SE elements, rows of GRS)
+    es, grs = {"f16s": (2, 2 * N), "split": (4, N), "bf16": (2, N)}[fmt]
+    rb = N * es
+    ppr, rpd = rb // 16, 1024 // rb
+    scopies = P // rpd // 8
+    ssw = (lambda r: r & 15) if ppr >= 16 else (lambda r: (r >> 1) & 7)
+    d = wave + 8 * np.arange(scopies)[:, None, None]
+    srow = rpd * d + lane // ppr
+    spiece = (lane % ppr) ^ ssw(wave * rpd + lane // ppr)
+    inside("S_in rows", srow, 0, P)
+    inside("S_in pieces within the stored row", spiece, 0, ppr)   # ppr * 16 bytes = the row's data
+    inside("S_in element within the row slot", spiece * (16 // es) + 16 // es - 1, 0, grs)
+    inside("S_in LDS", 1 * P * rb + d * 1024 + 16 * lane + 15, 0, 2 * P * rb)
+    # the ssw the copy uses (from the wave) is the row's own
+    assert (ssw(wave * rpd + lane // ppr) == ssw(srow)).all()
+    # scales, Acs, dt
+    inside("scales per item", lane, 0, P)
+    inside("Acs of the item", 4 * lane + 3, 0, Q)
+    inside("Acs LDS (one copy per wave)", wave * Q * 4 + 16 * lane + 15, 0, 8 * Q * 4)
+    dwave = np.arange(4)[:, None]
+    inside("dt rows in the chunk", 64 * dwave + lane, 0, Q)
+    inside("dt LDS", 1 * Q * 4 + 256 * dwave + 4 * lane + 3, 0, 2 * Q * 4)
+    # y stores (and the epilogue's z loads): rows 16 t + i, 8 columns from ycol + 32 pp
+    t = np.stack([wave, 15 - wave])
+    inside("y / z rows", 16 * t + i, 0, Q)
+    ycol = 8 * (g >> 1) + 16 * (g & 1)
+    pp = np.arange(2)[:, None, None]
+    inside("y / z columns", ycol + 32 * pp + 7, 0, P)
+    # C fragments (rows 16 t + i, columns 32 kc + 8 g .. + 7)
+    kc = np.arange(N // 32)[:, None, None]
+    inside("C columns", 32 * kc + 8 * g + 7, 0, N)
+    # chunk_prep's CB^T fragments: f32x4 index wbase * (9 * 2 * 64) + lane + (2 k + st) * 64
+    groups = B * nc * G
+    wbase = (np.arange(groups)[:, None] * 8 + np.arange(8)[None, :]).max()
+    k = np.arange(9)[:, None, None, None]
+    st = np.arange(2)[None, :, None, None]
+    cb32 = wbase * (9 * 2 * 64) + lane + (k * 2 + st) * 64
+    inside("CB^T f32 fragments", cb32, 0, groups * 8 * 9 * 2 * 64)
+    cb16 = wbase * (9 * 64) + lane + k * 64
+    inside("CB^T 16-bit fragments (16-byte units)", cb16, 0, groups * 8 * 9 * 2 * 64 // 2)
+
+
+# ---------------------------------------------------------------------------
+# chunk-256 persistent chunk_state and the state chain (ssd_chunk_state_q256.hip)
+# ---------------------------------------------------------------------------
+
+def chain_plan(chains, nchunks):
+    """chunk_state_chain_plan on a 256-CU device: (nfull, seg_per_chain, seg_len)."""
+    pin("ssd_chunk_state_q256.hip",
+        "if (4 * chains >= 3 * per_cu * cus) return ChainPlan{(int)chains, 1, a.nchunks};",
+        "const int64_t want = cus / rest > 1 ? cus / rest : 1;  // segments per chain",
+        "const int seg_len = (int)((a.nchunks + want - 1) / want);",
+        "const int segs = (a.nchunks + seg_len - 1) / seg_len;",
+        "return ChainPlan{(int)cus, segs, seg_len};")
+    per_cu = -(-chains // CUS)
+    if 4 * chains >= 3 * per_cu * CUS:
+        return chains, 1, nchunks
+    if CUS < chains < 2 * CUS:
+        rest = chains - CUS
+        want = max(CUS // rest, 1)
+        seg_len = -(-nchunks // want)
+        return CUS, -(-nchunks // seg_len), seg_len
+    return None
+
+
+@pytest.mark.parametrize("name", ["C3", "C4", "R0-layer"])
+def test_chunk_state_q256_and_chain_addresses(name):
+    B, L, H, P, N, Q, G, _ = SHAPES[name]
+    nc = L // Q
+    NT = N // 16
+    NK = N // 32
+    PTW = NT // 2
+    pin("ssd_chunk_state_q256.hip",
+        "const int nt = wave % NTILE, pt0 = (wave / NTILE) * PTW;",
+        "const int srow = (16 * pt0 + i) * N + 16 * nt + 4 * g;",
+        "const int blk = wave + kNW * m;",
+        "dma16_at(xg + (int64_t)(8 * blk) * p.sxl, xr_lds + (uint32_t)((hb * kQ * kP + blk * 512) * (int)sizeof(T)));",
+        "dma16_at(xchain + (l0 + 8 * blk) * p.sxl, xr_lds + (uint32_t)((bs * kQ * kP + blk * 512) * (int)sizeof(T)));",
+        "if (wave == kNW - 1) dma16_at(achain + (int64_t)c * kQ + 4 * lane, ar_lds + (uint32_t)(bs * kQ * 4));",
+        "if (wave < kQ / 64) dma4_at(dchain + (l0 + 64 * wave + lane) * p.sdl, dr_lds + (uint32_t)((bs * kQ + 64 * wave) * 4));",
+        "((((int64_t)b * p.nchunks + c) * p.ngroups + grp) * NTILE + nt) * (kKS * 64) + lane;",
+        "const frag8<T>* bnext = btf_of(has_next ? c + 1 : c);",
+        "*reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;",
+        "sp.sscale[(((int64_t)b * p.nchunks + c) * p.nheads + h) * kP + row] = __builtin_ldexpf(1.f, e);",
+        "bh = plan.nfull + sg / plan.seg_per_chain;",
+        "c0 = (sg % plan.seg_per_chain) * plan.seg_len;",
+        "c1 = min(c0 + plan.seg_len, p.nchunks);",
+        "if (c0 >= c1) return;  // the whole workgroup, before any barrier")
+    wave, lane = lanes()
+    g, i = lane >> 4, lane & 15
+    nt, pt0 = wave % NT, (wave // NT) * PTW
+    q = np.arange(PTW)[:, None, None]
+    # state tiles: rows 16 (pt0 + q) + i, columns 16 nt + 4 g .. + 3 (f32 [P][N])
+    inside("state rows", 16 * (pt0 + q) + i, 0, P)
+    inside("state columns", 16 * nt + 4 * g + 3, 0, N)
+    inside("f16s: f16 columns in the row's first half", 16 * nt + 4 * g + 3, 0, N)
+    inside("f16s scales rows", 16 * (pt0 + q) + i, 0, P)
+    # x copy parts, Acs, dt: as chunk_scan's (8-row blocks blk = wave + 8 m, m < 4)
+    blk = wave + 8 * np.arange(4)[:, None, None]
+    inside("x rows in the chunk", 8 * blk + (lane >> 3), 0, Q)
+    inside("chain x LDS (2 buffers)", 1 * Q * P * 2 + blk * 512 * 2 + 16 * lane + 15, 0, 2 * Q * P * 2)
+    inside("persistent x LDS ([2 halves][2 buffers])", 3 * Q * P * 2 + blk * 512 * 2 + 16 * lane + 15, 0, 4 * Q * P * 2)
+    inside("Acs", 4 * lane + 3, 0, Q)
+    inside("dt", 64 * np.arange(4)[:, None] + lane, 0, Q)
+    # B^T fragments: ((bcg * NTILE + nt) * 8 + ks) * 64 + lane frag8 units
+    groups = B * nc * G
+    ks = np.arange(8)[:, None, None]
+    inside("B^T fragments", ((groups - 1) * NT + nt) * (8 * 64) + ks * 64 + lane, 0, groups * NT * 8 * 64)
+    # the chain's workgroups: whole chains and segments, the chunks each walks
+    chains = B * H
+    plan = chain_plan(chains, nc)
+    if plan is None:
+        return
+    nfull, spc, seg_len = plan
+    grid = nfull + (chains - nfull) * spc
+    blocks = np.arange(grid)
+    local = blocks >= nfull
+    sg = blocks - nfull
+    bh = np.where(local, nfull + sg // spc, blocks)
+    c0 = np.where(local, (sg % spc) * seg_len, 0)
+    c1 = np.where(local, np.minimum(c0 + seg_len, nc), nc)
+    live = c0 < c1
+    inside("chain bh", bh[live], 0, chains)
+    inside("chain first chunk", c0[live], 0, nc)
+    inside("chain end chunk", c1[live], 1, nc + 1)
+    # every chunk of every chain walked exactly once
+    cover = np.zeros((chains, nc), np.int64)
+    for a, s, e in zip(bh[live], c0[live], c1[live]):
+        cover[a, s:e] += 1
+    assert (cover == 1).all()
+    # K2-then-K3 tail of the mixed plan: state_passing over chains [nfull, chains)
+    if nfull < chains:
+        inside("state_passing chains", np.arange(nfull, chains), 0, chains)
+
+
+# ---------------------------------------------------------------------------
+# chunk_prep (ssd_chunk_prep.hip)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", ["C3", "C4", "R0-layer"])
+def test_chunk_prep_addresses(name):
+    B, L, H, P, N, Q, G, _ = SHAPES[name]
+    pin("ssd_chunk_prep.hip",
+        "constexpr int RB = N * 2;",
+        "constexpr int RPD = 1024 / RB;",
+        "for (int d = wave; d < kQ / RPD; d += kNW) {",
+        "const int r = d * RPD + lane / PPR;",
+        "const int piece = (lane % PPR) ^ sw(r);",
+        "dma16_at(bg + (int64_t)r * p.sbl + 8 * piece, bl_lds + (uint32_t)(d * 1024));",
+        "const int ta = wave, tb = 15 - wave, KA = ta / 2 + 1;",
+        "cf[0][kc] = load8<T>(cg + (int64_t)(16 * ta + i) * p.scl + 8 * (4 * kc + g));",
+        "f32x4* out = reinterpret_cast<f32x4*>(p.cbf) + (int64_t)(bcg * kNW + wave) * kNPair * 2 * 64 + lane;",
+        "frag8<T>* bt_out = reinterpret_cast<frag8<T>*>(p.btf) + (int64_t)bcg * NTILE * 8 * 64 + lane;",
+        "for (int f = wave; f < NTILE * 8; f += kNW) {")
+    rb = 2 * N
+    ppr, rpd = rb // 16, 1024 // rb
+    sw = (lambda r: r & 15) if ppr >= 16 else (lambda r: (r >> 1) & 7)
+    wave, lane = lanes()
+    g, i = lane >> 4, lane & 15
+    d = np.arange(Q // rpd)
+    r = d[:, None] * rpd + lane // ppr
+    inside("B rows", r, 0, Q)
+    inside("B elements", 8 * ((lane % ppr) ^ sw(r)) + 7, 0, N)
+    inside("B LDS", d[:, None] * 1024 + 16 * lane + 15, 0, Q * rb)
+    inside("C rows", 16 * np.stack([wave, 15 - wave]) + i, 0, Q)
+    inside("C columns", 8 * (4 * np.arange(N // 32)[:, None, None] + g) + 7, 0, N)
+    groups = B * (L // Q) * G
+    bcg = groups - 1
+    k = np.arange(9)[:, None, None, None]
+    st = np.arange(2)[None, :, None, None]
+    inside("CB^T out", (bcg * 8 + wave) * 9 * 2 * 64 + lane + (k * 2 + st) * 64, 0, groups * 8 * 9 * 2 * 64)
+    f = np.arange(N // 16 * 8)[:, None]
+    inside("B^T out", bcg * (N // 16) * 8 * 64 + lane + f * 64, 0, groups * (N // 16) * 8 * 64)
+
+
+# ---------------------------------------------------------------------------
+# f32 chunk_scan and chunk_state / state chain at chunk 64 / 128
+# (ssd_chunk_scan_f32.hip, ssd_chunk_state_f32.hip)
+# ---------------------------------------------------------------------------
+
+def f32_units(B, L, H, Q, G):
+    """launch_qn's units (b, c, group, head slice) and their heads."""
+    pin("ssd_chunk_scan_f32.hip",
+        "int slices = (int)((cus + bcg - 1) / bcg);",
+        "const int hs = (hpg + slices - 1) / slices;",
+        "slices = (hpg + hs - 1) / hs;",
+        "const int h0 = grp * hpg + slice * hs;",
+        "const int h1 = min(h0 + hs, (grp + 1) * hpg);")
+    hpg = H // G
+    bcg = B * (L // Q) * G
+    slices = min(max(-(-CUS // bcg), 1), hpg)
+    hs = -(-hpg // slices)
+    slices = -(-hpg // hs)
+    u = np.arange(bcg * slices)
+    slice_, bcgi = u % slices, u // slices
+    grp = bcgi % G
+    h0 = grp * hpg + slice_ * hs
+    h1 = np.minimum(h0 + hs, (grp + 1) * hpg)
+    cover = np.zeros((bcg, H), np.int64)
+    for k, a, e in zip(bcgi, h0, h1):
+        cover[k, a:e] += 1
+    # every (b, c) sees every head exactly once, within its group's heads
+    assert (cover.reshape(B * (L // Q), G, H).sum(1) == 1).all()
+    return h0, h1
+
+
+@pytest.mark.parametrize("name", ["C2", "C5"])
+def test_f32_kernel_addresses(name):
+    B, L, H, P, N, Q, G, _ = SHAPES[name]
+    assert P == 64 and Q in (64, 128) and N in (64, 128)
+    f32_units(B, L, H, Q, G)
+    RT = Q // 64
+    pin("ssd_chunk_scan_f32.hip",
+        "const int blk = wave + kNW * m, r = 4 * blk + (lane >> 4), pc = (lane & 15) ^ (4 * ((r >> 2) & 3));",
+        "dma16_at(xg + r * p.sxl + 4 * pc, xs_lds + (uint32_t)((bf * Q * kP + blk * 256) * 4));",
+        "const int blk = wave + kNW * m, r = blk * (64 / SPR) + lane / SPR, pc = (lane % SPR) ^ (r & 7);",
+        "dma16_at(sg + r * N + 4 * pc, ss_lds + (uint32_t)((bf * kP * N + blk * 256) * 4));",
+        "if (wave == kNW - 1 && lane < Q / 4) {",
+        "dma16_at(ag + 4 * lane, al_lds + (uint32_t)(bf * Q * 4));",
+        "const int part = wave - (kNW - 1 - Q / 64);",
+        "dma4_at(dg + (l0 + 64 * part + lane) * p.sdl, dl_lds + (uint32_t)((bf * Q + 64 * part) * 4));",
+        "float* yrow = yg + (int64_t)(16 * trow[r] + 4 * g + jj) * p.syl + 32 * ph + i;",
+        "for (int e = 0; e < 2; ++e) yrow[16 * e] = acc[r][e][jj];",
+        "const int ph = wave >> 2, rg = RT == 1 && ph ? 3 - (wave & 3) : wave & 3;",
+        "cf[r][kc] = load8<float>(cg + (16 * trow[r] + i) * p.scl + 32 * kc + 8 * g);",
+        "d = mma(load8<float>(bg + (32 * sb + 16 * st + i) * p.sbl + 32 * kc + 8 * g), cf[r][kc], d);")
+    pin("ssd_chunk_state_f32.hip",
+        "const int ppr = cols / 4, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ (4 * ((r >> 2) & 3));",
+        "dma16_at(src + r * ld + 4 * pc, dst + (uint32_t)(blk * 1024));",
+        "sg[(16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] = acc[a][n][jj];",
+        "sg[(16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] = st[a][n][jj];",
+        "const int pp = wave & 1, nt0 = (wave >> 1) * NTW;")
+    wave, lane = lanes()
+    g, i = lane >> 4, lane & 15
+    # x copies (chunk_scan, chunk_state, chain): 1 KB = 4 rows of 64 floats
+    xpw = Q * P // 256 // 8
+    blk = wave + 8 * np.arange(xpw)[:, None, None]
+    r = 4 * blk + (lane >> 4)
+    inside("x rows", r, 0, Q)
+    inside("x floats", 4 * ((lane & 15) ^ (4 * ((r >> 2) & 3))) + 3, 0, P)
+    inside("x LDS", (1 * Q * P + blk * 256) * 4 + 16 * lane + 15, 0, 2 * Q * P * 4)
+    # S_in copies (chunk_scan): rows of N floats, SPR pieces
+    spr = N // 4
+    spw = P * N // 256 // 8
+    sblk = wave + 8 * np.arange(spw)[:, None, None]
+    sr = sblk * (64 // spr) + lane // spr
+    inside("S_in rows", sr, 0, P)
+    inside("S_in floats", 4 * ((lane % spr) ^ (sr & 7)) + 3, 0, N)
+    inside("S_in LDS", (1 * P * N + sblk * 256) * 4 + 16 * lane + 15, 0, 2 * P * N * 4)
+    # B copies (chunk_state f32, chain): rows of N floats, generic row copy
+    ppr = N // 4
+    bpw = Q * N // 256 // 8
+    bblk = wave + 8 * np.arange(bpw)[:, None, None]
+    br = bblk * (64 // ppr) + lane // ppr
+    inside("B rows", br, 0, Q)
+    inside("B floats", 4 * ((lane % ppr) ^ (4 * ((br >> 2) & 3))) + 3, 0, N)
+    lds_f = max(2 * Q * P, Q * P + Q * N)
+    inside("chunk_state B staging LDS", Q * P * 4 + bblk * 1024 + 16 * lane + 15, 0, lds_f * 4)
+    inside("chain B LDS (2 buffers)", (1 * Q * N) * 4 + bblk * 1024 + 16 * lane + 15, 0, 2 * Q * N * 4)
+    # Acs and dt copies
+    inside("Acs (lanes < Q / 4)", 4 * np.arange(Q // 4) + 3, 0, Q)
+    part = np.arange(Q // 64)[:, None]
+    inside("dt", 64 * part + lane, 0, Q)
+    # y stores: rows 16 t + 4 g + jj (t from the wave's row group), columns 32 ph + i + 16 e
+    ph = wave >> 2
+    rg = np.where((RT == 1) & (ph > 0), 3 - (wave & 3), wave & 3)
+    trow = [rg] + ([7 - rg] if RT == 2 else [])
+    jj = np.arange(4)[:, None, None]
+    for t in trow:
+        inside("y rows", 16 * t + 4 * g + jj, 0, Q)
+        inside("C rows", 16 * t + i, 0, Q)
+    inside("y columns", 32 * ph + i + 16, 0, P)
+    inside("C / B columns", 32 * np.arange(N // 32)[:, None, None] + 8 * g + 7, 0, N)
+    # state stores (chunk_state f32, chain): rows 16 (2 pp + a) + 4 g + jj, columns 16 (nt0 + n) + i
+    pp, nt0 = wave & 1, (wave >> 1) * (N // 64)
+    a = np.arange(2)[:, None, None, None]
+    n = np.arange(N // 64)[None, :, None, None]
+    inside("state rows", 16 * (2 * pp + a) + 4 * g + jj[None], 0, P)
+    inside("state columns", 16 * (nt0 + n) + i, 0, N)
+
+
+# ---------------------------------------------------------------------------
+# state_passing (ssd_state_passing.hip)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("name", list(SHAPES))
+def test_state_passing_addresses(name):
+    B, L, H, P, N, Q, G, _ = SHAPES[name]
+    pin("ssd_state_passing.hip",
+        "const int bh = p.bh_begin + (int)blockIdx.x / blocks_per_bh;",
+        "const int v = (blockIdx.x % blocks_per_bh) * 256 + threadIdx.x;",
+        "if (v >= vec_per_bh) return;",
+        "const int row = v / TPR, col = 8 * (v % TPR);",
+        "*reinterpret_cast<f16x8*>(hrow + c * 2 * cstride) = hv;",
+        "const int c = min(c0 + u, nchunks - 1);")
+    PN = P * N
+    nc = L // Q
+    chains = B * H
+    for per_thread in (4, 8):  # f32 / split kernels, f16s kernel
+        vec = PN // per_thread
+        bpb = -(-vec // 256)
+        blocks = np.arange(chains * bpb)
+        bh = blocks // bpb
+        v = (blocks % bpb)[:, None] * 256 + np.arange(256)[None, :]
+        v = v[v < vec]
+        inside("chains", bh, 0, chains)
+        inside("state elements of a chain", per_thread * v + per_thread - 1, 0, PN)
+        if per_thread == 8 and N in (64, 128):
+            tpr = N // 8
+            row, col = v // tpr, 8 * (v % tpr)
+            inside("f16s rows", row, 0, P)
+            inside("f16s f16 columns (the row's first half)", col + 7, 0, N)
+    # the chunk index every (clamped) load of the pipelined chain uses
+    for nchunks in sorted({1, 2, 7, 16, 17, nc}):
+        c0 = np.arange(0, nchunks + 16, 8)
+        c = np.minimum(c0[:, None] + np.arange(8)[None, :], nchunks - 1)
+        inside("chain chunk", c, 0, nchunks)
