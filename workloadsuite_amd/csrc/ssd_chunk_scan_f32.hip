@@ -239,7 +239,16 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_f32_kernel(ChunkScanArgs 
           }
         }
 #pragma unroll
-        for (int e = 0; e < 2; ++e) acc[r][e] = mma(af, xf[e], acc[r][e]);
+        for (int e = 0; e < 2; ++e) {
+          if (2 * sb + 1 > t) {
+            // the block's second 16 tokens lie wholly above the diagonal (their
+            // slots of af are zero): only the first half's MFMAs, same sums
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[r][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[j], xf[e][j], acc[r][e], 0, 0, 0);
+          } else {
+            acc[r][e] = mma(af, xf[e], acc[r][e]);
+          }
+        }
       }
     }
     dma_wait();
