@@ -454,13 +454,15 @@ def test_state_passing_addresses(name):
         "const int bh = p.bh_begin + (int)blockIdx.x / blocks_per_bh;",
         "const int v = (blockIdx.x % blocks_per_bh) * 256 + threadIdx.x;",
         "if (v >= vec_per_bh) return;",
-        "const int row = v / TPR, col = 8 * (v % TPR);",
-        "*reinterpret_cast<f16x8*>(hrow + c * 2 * cstride) = hv;",
+        "const int row = v / TPR, col = SPT * (v % TPR);",
+        "float* elem = base + SPT * (int64_t)v;",
+        "*reinterpret_cast<H*>(hrow + c * 2 * cstride) = hv;",
+        "constexpr int spt = 4;",
         "const int c = min(c0 + u, nchunks - 1);")
     PN = P * N
     nc = L // Q
     chains = B * H
-    for per_thread in (4, 8):  # f32 / split kernels, f16s kernel
+    for per_thread in (4,):  # f32 / split kernels and the f16s kernel (spt)
         vec = PN // per_thread
         bpb = -(-vec // 256)
         blocks = np.arange(chains * bpb)
@@ -469,13 +471,14 @@ def test_state_passing_addresses(name):
         v = v[v < vec]
         inside("chains", bh, 0, chains)
         inside("state elements of a chain", per_thread * v + per_thread - 1, 0, PN)
-        if per_thread == 8 and N in (64, 128):
-            tpr = N // 8
-            row, col = v // tpr, 8 * (v % tpr)
+        if N in (64, 128):
+            tpr = N // per_thread
+            row, col = v // tpr, per_thread * (v % tpr)
             inside("f16s rows", row, 0, P)
-            inside("f16s f16 columns (the row's first half)", col + 7, 0, N)
-    # the chunk index every (clamped) load of the pipelined chain uses
-    for nchunks in sorted({1, 2, 7, 16, 17, nc}):
-        c0 = np.arange(0, nchunks + 16, 8)
-        c = np.minimum(c0[:, None] + np.arange(8)[None, :], nchunks - 1)
-        inside("chain chunk", c, 0, nchunks)
+            inside("f16s f16 columns (the row's first half)", col + per_thread - 1, 0, N)
+    # the chunk index every (clamped) load of the pipelined chain uses (batches of 4 or 8)
+    for unroll in (4, 8):
+        for nchunks in sorted({1, 2, 7, 16, 17, nc}):
+            c0 = np.arange(0, nchunks + 2 * unroll, unroll)
+            c = np.minimum(c0[:, None] + np.arange(unroll)[None, :], nchunks - 1)
+            inside("chain chunk", c, 0, nchunks)

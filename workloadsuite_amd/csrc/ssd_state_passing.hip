@@ -27,7 +27,6 @@ namespace ssd {
 
 namespace {
 
-constexpr int kUnroll = 8;
 
 template <typename S> struct StateIO;
 // Local states are read once.  Long chains read them with non-temporal loads
@@ -63,7 +62,7 @@ template <> struct StateIO<bf16> {
 // of loads in flight (two register batches used in turn: no copies between
 // them, which would wait for the loads).  load(c) returns chunk c's local
 // state, store(c, v) writes S_in[c] = v; dec[c] is chunk c's decay.
-template <typename V, typename LoadF, typename StoreF>
+template <int kUnroll = 8, typename V, typename LoadF, typename StoreF>
 __device__ __forceinline__ V run_chain(int nchunks, const float* __restrict__ dec, V st, LoadF load,
                                        StoreF store) {
   V la[kUnroll], lb[kUnroll];
@@ -194,7 +193,7 @@ __global__ __launch_bounds__(256) void state_passing_split_kernel(StatePassingAr
 // then the half-row and row mirrors.
 template <int G>
 __device__ __forceinline__ float row_max(float m) {
-  static_assert(G == 8 || G == 16, "lane group");
+  static_assert(G == 8 || G == 16 || G == 32, "lane group");
   auto dpp = [](float v, int ctrl) __attribute__((always_inline)) {
     switch (ctrl) {
       case 0: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));   // quad 1,0,3,2
@@ -206,7 +205,12 @@ __device__ __forceinline__ float row_max(float m) {
   m = fmaxf(m, dpp(m, 0));
   m = fmaxf(m, dpp(m, 1));
   m = fmaxf(m, dpp(m, 2));
-  if constexpr (G == 16) m = fmaxf(m, dpp(m, 3));
+  if constexpr (G >= 16) m = fmaxf(m, dpp(m, 3));
+  if constexpr (G == 32) {
+    // with the neighbouring 16-lane row
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  }
   return m;
 }
 
@@ -214,69 +218,74 @@ __device__ __forceinline__ float row_max(float m) {
 // scale per state row (SSD_STATE_F16S), the f16 values written in place in
 // the f32 layout: row p of an item (N f32 slots) gets its N f16 values,
 // v / 2^e, in its first half, and 2^e goes to sscale[item][p]; e is chosen
-// so that the row's largest |v| lies in [2^14, 2^15].  Each thread owns 8
-// consecutive states of a row (two 16-byte loads per chunk, one 16-byte
-// store); the N/8 threads of a row (one wave holds whole rows) find the row's
-// largest magnitude with DPP moves.  Every load of a row precedes, in the
-// wave's instruction order, the stores into that row, so the in-place writes
-// never overtake a read.  The recurrence and final_state stay f32.
-template <int N>
+// so that the row's largest |v| lies in [2^14, 2^15].  Each thread owns SPT
+// consecutive states of a row (16-byte loads per chunk, one 2 SPT-byte
+// store); the N/SPT threads of a row (one wave holds whole rows) find the
+// row's largest magnitude with DPP moves (and a 16-lane row swap for 32
+// threads).  Every load of a row precedes, in the wave's instruction order,
+// the stores into that row, so the in-place writes never overtake a read.
+// The recurrence and final_state stay f32.
+template <int N, int SPT, int UNROLL>
 __global__ __launch_bounds__(256) void state_passing_f16s_kernel(StatePassingArgs p) {
-  constexpr int TPR = N / 8;  // threads per row
+  constexpr int TPR = N / SPT;  // threads per row (SPT = 4 or 8 states per thread)
+  typedef typename std::conditional<SPT == 8, f32x8, f32x4>::type V;
+  typedef typename std::conditional<SPT == 8, f16x8, f16x4>::type H;
   const int64_t PN = (int64_t)p.headdim * N;
-  const int vec_per_bh = (int)(PN / 8);
+  const int vec_per_bh = (int)(PN / SPT);
   const int blocks_per_bh = (vec_per_bh + 255) / 256;
   const int bh = p.bh_begin + (int)blockIdx.x / blocks_per_bh;
   const int v = (blockIdx.x % blocks_per_bh) * 256 + threadIdx.x;
   if (v >= vec_per_bh) return;  // vec_per_bh is a multiple of 256: whole waves leave together
   const int h = bh % p.nheads, b = bh / p.nheads;
-  const int row = v / TPR, col = 8 * (v % TPR);
+  const int row = v / TPR, col = SPT * (v % TPR);
 
   float* base = reinterpret_cast<float*>(p.states) + ((int64_t)b * p.nchunks * p.nheads + h) * PN;
   const int64_t cstride = (int64_t)p.nheads * PN;
   const float* dec = p.decay + (int64_t)bh * p.nchunks;
-  float* elem = base + 8 * (int64_t)v;                       // this thread's 8 f32 states
-  f16* hrow = reinterpret_cast<f16*>(base + (int64_t)row * N) + col;  // its 8 f16 slots
+  float* elem = base + SPT * (int64_t)v;                     // this thread's f32 states
+  f16* hrow = reinterpret_cast<f16*>(base + (int64_t)row * N) + col;  // its f16 slots
   // the row's scale: sscale[b, c, h, row], chunks p.nheads * headdim apart
   float* srow = p.sscale + ((int64_t)b * p.nchunks * p.nheads + h) * p.headdim + row;
   const int64_t sstride = (int64_t)p.nheads * p.headdim;
 
-  f32x8 st;
-  if (p.init) {
-    st.lo = *reinterpret_cast<const f32x4*>(p.init + (int64_t)bh * PN + 8 * (int64_t)v);
-    st.hi = *reinterpret_cast<const f32x4*>(p.init + (int64_t)bh * PN + 8 * (int64_t)v + 4);
-  } else {
-    st = f32x8{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  }
-  auto store_f16s = [&](int c, f32x8 val) {
-    asm volatile("" : "+v"(val));  // from the f32 state (no fusing of the recurrence into the rounding)
-    float m = 0.f;
+  // SPT consecutive floats from p (16-byte loads), non-temporal or not
+  auto loadv = [](const float* src, auto nt) __attribute__((always_inline)) {
+    const f32x4* q = reinterpret_cast<const f32x4*>(src);
+    V r;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) m = fmaxf(m, fabsf(val[k]));
-    m = row_max<TPR>(m);
-    const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
-    f16x8 hv;
+    for (int h = 0; h < SPT / 4; ++h) {
+      const f32x4 x = decltype(nt)::value ? __builtin_nontemporal_load(q + h) : q[h];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) hv[k] = (f16)__builtin_ldexpf(val[k], -e);
-    *reinterpret_cast<f16x8*>(hrow + c * 2 * cstride) = hv;
-    if (col == 0) srow[c * sstride] = __builtin_ldexpf(1.f, e);
-  };
-  auto load8f = [&](int c, auto nt) {
-    const f32x4* q = reinterpret_cast<const f32x4*>(elem + c * cstride);
-    f32x8 r;
-    if constexpr (decltype(nt)::value) {
-      r.lo = __builtin_nontemporal_load(q);
-      r.hi = __builtin_nontemporal_load(q + 1);
-    } else {
-      r.lo = q[0];
-      r.hi = q[1];
+      for (int k = 0; k < 4; ++k) r[4 * h + k] = x[k];
     }
     return r;
   };
-  st = run_chain(p.nchunks, dec, st, load8f, store_f16s);
+  V st;
+  if (p.init) {
+    st = loadv(p.init + (int64_t)bh * PN + SPT * (int64_t)v, std::false_type());
+  } else {
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) st[k] = 0.f;
+  }
+  auto store_f16s = [&](int c, V val) {
+    asm volatile("" : "+v"(val));  // from the f32 state (no fusing of the recurrence into the rounding)
+    float m = 0.f;
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) m = fmaxf(m, fabsf(val[k]));
+    m = row_max<TPR>(m);
+    const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
+    H hv;
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) hv[k] = (f16)__builtin_ldexpf(val[k], -e);
+    *reinterpret_cast<H*>(hrow + c * 2 * cstride) = hv;
+    if (col == 0) srow[c * sstride] = __builtin_ldexpf(1.f, e);
+  };
+  st = run_chain<UNROLL>(p.nchunks, dec, st, [&](int c, auto nt) { return loadv(elem + c * cstride, nt); }, store_f16s);
   if (p.final_state) {
-    *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * PN + 8 * (int64_t)v) = st.lo;
-    *reinterpret_cast<f32x4*>(p.final_state + (int64_t)bh * PN + 8 * (int64_t)v + 4) = st.hi;
+    float* fo = p.final_state + (int64_t)bh * PN + SPT * (int64_t)v;
+#pragma unroll
+    for (int h = 0; h < SPT / 4; ++h)
+      *reinterpret_cast<f32x4*>(fo + 4 * h) = f32x4{st[4 * h], st[4 * h + 1], st[4 * h + 2], st[4 * h + 3]};
   }
 }
 
@@ -288,11 +297,15 @@ hipError_t launch_state_passing(const StatePassingArgs& a, int state_dtype, hipS
   if (a.bh_begin < 0 || a.bh_count < 0 || a.bh_begin + (int64_t)a.bh_count > all) return hipErrorInvalidValue;
   const int64_t chains = a.bh_count > 0 ? a.bh_count : all - a.bh_begin;
   if (a.f16s) {
-    if (state_dtype != SSD_DTYPE_F32 || a.split_dtype != 0 || !a.sscale || (PN / 8) % 256 != 0)
+    // 4 states per thread and batches of 4 chunks: 75 VGPRs, so the 80 chains
+    // of C4 fit the device in one wave of workgroups (8 states per thread and
+    // batches of 8: 196 VGPRs, 0.53 instead of 0.58 of HBM peak at C4)
+    constexpr int spt = 4;
+    if (state_dtype != SSD_DTYPE_F32 || a.split_dtype != 0 || !a.sscale || (PN / spt) % 256 != 0)
       return hipErrorInvalidValue;
-    const dim3 grid((unsigned)(chains * ((PN / 8 + 255) / 256)));
-    if (a.dstate == 128) state_passing_f16s_kernel<128><<<grid, 256, 0, stream>>>(a);
-    else if (a.dstate == 64) state_passing_f16s_kernel<64><<<grid, 256, 0, stream>>>(a);
+    const dim3 grid((unsigned)(chains * ((PN / spt + 255) / 256)));
+    if (a.dstate == 128) state_passing_f16s_kernel<128, spt, 4><<<grid, 256, 0, stream>>>(a);
+    else if (a.dstate == 64) state_passing_f16s_kernel<64, spt, 4><<<grid, 256, 0, stream>>>(a);
     else return hipErrorInvalidValue;
     return hipGetLastError();
   }
