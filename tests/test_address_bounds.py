@@ -383,16 +383,21 @@ def test_f32_kernel_addresses(name):
         "dma16_at(ag + 4 * lane, al_lds + (uint32_t)(bf * Q * 4));",
         "const int part = wave - (kNW - 1 - Q / 64);",
         "dma4_at(dg + (l0 + 64 * part + lane) * p.sdl, dl_lds + (uint32_t)((bf * Q + 64 * part) * 4));",
-        "float* yrow = yg + (int64_t)(16 * trow[r] + 4 * g + jj) * p.syl + 32 * ph + i;",
-        "for (int e = 0; e < 2; ++e) yrow[16 * e] = acc[r][e][jj];",
+        "*reinterpret_cast<f32x4*>(yg + (int64_t)(16 * trow[r] + i) * p.syl + 16 * (2 * ph + e) + 4 * g) = acc[r][e];",
         "const int ph = wave >> 2, rg = RT == 1 && ph ? 3 - (wave & 3) : wave & 3;",
         "cf[r][kc] = load8<float>(cg + (16 * trow[r] + i) * p.scl + 32 * kc + 8 * g);",
-        "d = mma(load8<float>(bg + (32 * sb + 16 * st + i) * p.sbl + 32 * kc + 8 * g), cf[r][kc], d);")
+        "const uint32_t bt_lds = kBinX ? xs_lds + Q * kP * 4 : ss_lds + kP * N * 4;",
+        "dma16_at(bg + r * p.sbl + 4 * pc, bt_lds + (uint32_t)(blk * 1024));",
+        "const int row = 32 * sb + 16 * st + i, pc = 8 * kc + 2 * g;",
+        "bf8.hi = *reinterpret_cast<const f32x4*>(brow + 4 * ((pc + 1) ^ (row & 7)));")
     pin("ssd_chunk_state_f32.hip",
         "const int ppr = cols / 4, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ (4 * ((r >> 2) & 3));",
         "dma16_at(src + r * ld + 4 * pc, dst + (uint32_t)(blk * 1024));",
-        "sg[(16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] = acc[a][n][jj];",
-        "sg[(16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] = st[a][n][jj];",
+        "*reinterpret_cast<f32x4*>(sg + (16 * (2 * pp + a) + i) * N + 16 * (nt0 + n) + 4 * g) = acc[a][n];",
+        "return (16 * (2 * pp + a) + i) * N + 16 * (nt0 + n) + 4 * g;",
+        "*reinterpret_cast<f32x4*>(sg + sidx(a, n)) = st[a][n];",
+        "*reinterpret_cast<const f32x4*>(sp.init + bh * PN + sidx(a, n))",
+        "*reinterpret_cast<f32x4*>(sp.final_state + bh * PN + sidx(a, n)) = st[a][n];",
         "const int pp = wave & 1, nt0 = (wave >> 1) * NTW;")
     wave, lane = lanes()
     g, i = lane >> 4, lane & 15
@@ -411,6 +416,23 @@ def test_f32_kernel_addresses(name):
     inside("S_in rows", sr, 0, P)
     inside("S_in floats", 4 * ((lane % spr) ^ (sr & 7)) + 3, 0, N)
     inside("S_in LDS", (1 * P * N + sblk * 256) * 4 + 16 * lane + 15, 0, 2 * P * N * 4)
+    # B copies (chunk_scan): rows of N floats, SPR pieces, into x's second
+    # buffer when N <= 64, else S_in's (Q = 64 there); C.B^T reads rows
+    # 32 sb + 16 st + i < Q
+    bpw = Q * N // 256 // 8
+    tblk = wave + 8 * np.arange(bpw)[:, None, None]
+    tr = tblk * (64 // spr) + lane // spr
+    inside("chunk_scan B rows", tr, 0, Q)
+    inside("chunk_scan B floats", 4 * ((lane % spr) ^ (tr & 7)) + 3, 0, N)
+    if N <= P:
+        inside("chunk_scan B LDS (x buffer 1)", Q * P * 4 + tblk * 1024 + 16 * lane + 15, Q * P * 4, 2 * Q * P * 4)
+    else:
+        assert Q == 64
+        inside("chunk_scan B LDS (S_in buffer 1)", P * N * 4 + tblk * 1024 + 16 * lane + 15, P * N * 4, 2 * P * N * 4)
+    sb_, st_ = np.arange(2 * RT)[:, None, None, None], np.arange(2)[None, :, None, None]
+    inside("chunk_scan B fragment rows", 32 * sb_ + 16 * st_ + i, 0, Q)
+    bpc = 8 * np.arange(N // 32)[:, None, None, None] + 2 * g[..., None] + np.arange(2)
+    inside("chunk_scan B fragment floats", 4 * (bpc[..., None] ^ np.arange(8)) + 3, 0, N)
     # B copies (chunk_state f32, chain): rows of N floats, generic row copy
     ppr = N // 4
     bpw = Q * N // 256 // 8
@@ -425,22 +447,23 @@ def test_f32_kernel_addresses(name):
     inside("Acs (lanes < Q / 4)", 4 * np.arange(Q // 4) + 3, 0, Q)
     part = np.arange(Q // 64)[:, None]
     inside("dt", 64 * part + lane, 0, Q)
-    # y stores: rows 16 t + 4 g + jj (t from the wave's row group), columns 32 ph + i + 16 e
+    # y stores (4 floats): rows 16 t + i (t from the wave's row group), columns 16 (2 ph + e) + 4 g .. + 3
     ph = wave >> 2
     rg = np.where((RT == 1) & (ph > 0), 3 - (wave & 3), wave & 3)
     trow = [rg] + ([7 - rg] if RT == 2 else [])
     jj = np.arange(4)[:, None, None]
     for t in trow:
-        inside("y rows", 16 * t + 4 * g + jj, 0, Q)
+        inside("y rows", 16 * t + i, 0, Q)
         inside("C rows", 16 * t + i, 0, Q)
-    inside("y columns", 32 * ph + i + 16, 0, P)
+    inside("y columns", 16 * (2 * ph + np.arange(2)[:, None, None]) + 4 * g + 3, 0, P)
     inside("C / B columns", 32 * np.arange(N // 32)[:, None, None] + 8 * g + 7, 0, N)
-    # state stores (chunk_state f32, chain): rows 16 (2 pp + a) + 4 g + jj, columns 16 (nt0 + n) + i
+    # state stores, init and final state loads / stores (chunk_state f32,
+    # chain; 4 floats): rows 16 (2 pp + a) + i, columns 16 (nt0 + n) + 4 g .. + 3
     pp, nt0 = wave & 1, (wave >> 1) * (N // 64)
     a = np.arange(2)[:, None, None, None]
     n = np.arange(N // 64)[None, :, None, None]
-    inside("state rows", 16 * (2 * pp + a) + 4 * g + jj[None], 0, P)
-    inside("state columns", 16 * (nt0 + n) + i, 0, N)
+    inside("state rows", 16 * (2 * pp + a) + i, 0, P)
+    inside("state columns", 16 * (nt0 + n) + 4 * g + 3, 0, N)
 
 
 # ---------------------------------------------------------------------------

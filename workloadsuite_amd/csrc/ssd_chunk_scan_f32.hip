@@ -17,10 +17,14 @@
 // (so the two waves of each SIMD together hold three diagonal blocks), at
 // chunk 128 t = w % 4 and 7 - w % 4 (five blocks for every wave) -- and p
 // tiles 2 (w / 4) and 2 (w / 4) + 1.  Per wave and for the whole slice of
-// heads: C fragments of its rows (the A operand of C.S^T and the B operand of
-// C.B^T) and the raw C.B^T sub-tiles [s][l] of its rows in the D layout (4
-// consecutive s per lane), which with the decay, the causal mask and dt
-// applied are directly the A operand of the diagonal product.
+// heads: C fragments of its rows (the B operand of S.C^T and of C.B^T) and
+// the raw C.B^T sub-tiles [s][l] of its rows in the D layout (4 consecutive s
+// per lane), which with the decay, the causal mask and dt applied are
+// directly the B operand of the diagonal product.  S_in and x are the A
+// operands, so the accumulators hold y^T: each lane holds 4 consecutive p of
+// one token and writes them as one 16-byte store.  The chunk's B rows reach
+// the C.B^T products through LDS (one global -> LDS copy per slice, waited
+// for once) rather than as global loads per sub-tile.
 // Per head, x [s][p] and S_in [p][n] of the head are copied global -> LDS
 // (global_load_lds, rows XOR-swizzled by 16-byte piece so the operand reads
 // are free of bank conflicts) one head ahead, with Acs and dt.
@@ -108,6 +112,17 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_f32_kernel(ChunkScanArgs 
     }
   };
   issue_head(h0, 0);
+  // B rows of the chunk (N floats, pieces swizzled as S_in's) into the second
+  // copy buffer -- x's when N <= 64, else S_in's (then Q = 64): Q N floats
+  // either way -- free until the first head issues the second head's copies
+  constexpr bool kBinX = N <= kP;
+  constexpr int BPW = Q * N / 256 / kNW;
+  const uint32_t bt_lds = kBinX ? xs_lds + Q * kP * 4 : ss_lds + kP * N * 4;
+#pragma unroll
+  for (int m = 0; m < BPW; ++m) {
+    const int blk = wave + kNW * m, r = blk * (64 / SPR) + lane / SPR, pc = (lane % SPR) ^ (r & 7);
+    dma16_at(bg + r * p.sbl + 4 * pc, bt_lds + (uint32_t)(blk * 1024));
+  }
 
   // ---- per slice: C fragments and raw C.B^T sub-tiles of this wave's rows ----
   frag8<float> cf[RT][NK];
@@ -115,6 +130,9 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_f32_kernel(ChunkScanArgs 
   for (int r = 0; r < RT; ++r)
 #pragma unroll
     for (int kc = 0; kc < NK; ++kc) cf[r][kc] = load8<float>(cg + (16 * trow[r] + i) * p.scl + 32 * kc + 8 * g);
+  dma_wait();
+  __syncthreads();
+  const float* bt = kBinX ? xs[1] : ss[1];
   // cbr[r][sb][st][jj] = C.B^T[s = 32 sb + 16 st + 4 g + jj][l = 16 t + i]
   f32x4 cbr[RT][NSB][2];
 #pragma unroll
@@ -127,28 +145,32 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_f32_kernel(ChunkScanArgs 
         f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
         if (32 * sb + 16 * st <= 16 * t) {  // not entirely above the diagonal (wave-uniform)
 #pragma unroll
-          for (int kc = 0; kc < NK; ++kc)
-            d = mma(load8<float>(bg + (32 * sb + 16 * st + i) * p.sbl + 32 * kc + 8 * g), cf[r][kc], d);
+          for (int kc = 0; kc < NK; ++kc) {
+            const int row = 32 * sb + 16 * st + i, pc = 8 * kc + 2 * g;
+            const float* brow = bt + row * N;
+            frag8<float> bf8;
+            bf8.lo = *reinterpret_cast<const f32x4*>(brow + 4 * (pc ^ (row & 7)));
+            bf8.hi = *reinterpret_cast<const f32x4*>(brow + 4 * ((pc + 1) ^ (row & 7)));
+            d = mma(bf8, cf[r][kc], d);
+          }
         }
         cbr[r][sb][st] = d;
       }
   }
-  dma_wait();
-  __syncthreads();
+  __syncthreads();  // B's buffer takes the second head's copies from here on
 
   f32x4 acc[RT][2];
   int hprev = -1;
-  // y[l][p] of head hy from acc (rows 16 t + 4 g + jj, columns 16 pt + i)
+  // y of head hy from acc, which holds y^T (the S_in / x side is the MFMA's
+  // A operand): rows p = 16 pt + 4 g + jj, columns l = 16 t + i, so each lane
+  // writes 4 consecutive p of one token
   auto store_y = [&](int hy) __attribute__((always_inline)) {
     float* yg = yg0 + hy * p.syh;
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        float* yrow = yg + (int64_t)(16 * trow[r] + 4 * g + jj) * p.syl + 32 * ph + i;
-#pragma unroll
-        for (int e = 0; e < 2; ++e) yrow[16 * e] = acc[r][e][jj];
-      }
+      for (int e = 0; e < 2; ++e)
+        *reinterpret_cast<f32x4*>(yg + (int64_t)(16 * trow[r] + i) * p.syl + 16 * (2 * ph + e) + 4 * g) = acc[r][e];
   };
 
   for (int h = h0; h < h1; ++h) {
@@ -162,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_f32_kernel(ChunkScanArgs 
     const float* sb_ = ss[bf];
     const float* ab = al[bf];
 
-    // ---- off-diagonal: acc[l, p] = exp(Acs[l]) sum_n C[l, n] S_in[p, n] ----
+    // ---- off-diagonal: acc[p, l] = exp(Acs[l]) sum_n S_in[p, n] C[l, n] ----
 #pragma unroll
     for (int r = 0; r < RT; ++r)
 #pragma unroll
@@ -177,23 +199,19 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_f32_kernel(ChunkScanArgs 
         sf.lo = *reinterpret_cast<const f32x4*>(srow + 4 * (pc ^ (row & 7)));
         sf.hi = *reinterpret_cast<const f32x4*>(srow + 4 * ((pc + 1) ^ (row & 7)));
 #pragma unroll
-        for (int r = 0; r < RT; ++r) acc[r][e] = mma(cf[r][kc], sf, acc[r][e]);
+        for (int r = 0; r < RT; ++r) acc[r][e] = mma(sf, cf[r][kc], acc[r][e]);
       }
+    // log2(e) Acs[l] of this lane's token l = 16 t + i in each row tile
+    float all[RT];
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
-      const f32x4 a4 = *reinterpret_cast<const f32x4*>(ab + 16 * trow[r] + 4 * g);
+      all[r] = ab[16 * trow[r] + i] * kLog2e;
+      const float e = __builtin_amdgcn_exp2f(all[r]);
 #pragma unroll
-      for (int jj = 0; jj < 4; ++jj) {
-        const float e = __builtin_amdgcn_exp2f(a4[jj] * kLog2e);
-#pragma unroll
-        for (int ee = 0; ee < 2; ++ee) acc[r][ee][jj] *= e;
-      }
+      for (int ee = 0; ee < 2; ++ee) acc[r][ee] *= e;
     }
 
     // ---- diagonal: 32 tokens s per block; row tile t needs blocks sb <= t / 2 ----
-    float all[RT];
-#pragma unroll
-    for (int r = 0; r < RT; ++r) all[r] = ab[16 * trow[r] + i] * kLog2e;
 #pragma unroll
     for (int sb = 0; sb < NSB; ++sb) {
       if (sb > trow[RT - 1] / 2) continue;  // wave-uniform
@@ -244,9 +262,9 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_f32_kernel(ChunkScanArgs 
             // the block's second 16 tokens lie wholly above the diagonal (their
             // slots of af are zero): only the first half's MFMAs, same sums
 #pragma unroll
-            for (int j = 0; j < 4; ++j) acc[r][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[j], xf[e][j], acc[r][e], 0, 0, 0);
+            for (int j = 0; j < 4; ++j) acc[r][e] = __builtin_amdgcn_mfma_f32_16x16x4f32(xf[e][j], af[j], acc[r][e], 0, 0, 0);
           } else {
-            acc[r][e] = mma(af, xf[e], acc[r][e]);
+            acc[r][e] = mma(xf[e], af, acc[r][e]);
           }
         }
       }

@@ -17,6 +17,9 @@
 // Work decomposition: 8 waves; wave w owns p tiles 2 (w % 2), 2 (w % 2) + 1
 // and n tiles [(w / 2) N / 64, (w / 2 + 1) N / 64).  K index slot (g, j) of
 // K step ks is token l = 32 ks + 16 (j / 4) + 4 g + j % 4 in both operands.
+// B is the MFMA's A operand and the weighted x its B operand, so the
+// accumulators hold S^T: each lane holds 4 consecutive n of one p and stores
+// them as one 16-byte store.
 #include "ssd_device.h"
 #include "ssd_launch.h"
 #include "../../include/ssd.h"
@@ -119,16 +122,16 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
 
   f32x4 acc[2][NTW];
   int hprev = -1;
-  // states[b, c, h, p, n] of head hs_ from acc (rows p = 16 pt + 4 g + jj, columns n = 16 nt + i)
+  // states[b, c, h, p, n] of head hst from acc, which holds S^T (B is the
+  // MFMA's A operand): rows n = 16 nt + 4 g + jj, columns p = 16 pt + i, so
+  // each lane writes 4 consecutive n of one p as one 16-byte store
   auto store_states = [&](int hst) __attribute__((always_inline)) {
     float* sg = reinterpret_cast<float*>(p.states) + (((int64_t)b * p.nchunks + c) * p.nheads + hst) * (kP * N);
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int n = 0; n < NTW; ++n)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-          sg[(16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] = acc[a][n][jj];
+        *reinterpret_cast<f32x4*>(sg + (16 * (2 * pp + a) + i) * N + 16 * (nt0 + n) + 4 * g) = acc[a][n];
   };
 
   for (int h = h0; h < h1; ++h) {
@@ -165,7 +168,7 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
 #pragma unroll
         for (int j = 0; j < 8; ++j) xf[j] = xb[swz_off(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)] * w[j];
 #pragma unroll
-        for (int n = 0; n < NTW; ++n) acc[a][n] = mma(xf, bfr[n][ks], acc[a][n]);
+        for (int n = 0; n < NTW; ++n) acc[a][n] = mma(bfr[n][ks], xf, acc[a][n]);
       }
     }
     dma_wait();
@@ -236,35 +239,51 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
     }
   };
 
-  // running state: S_in of the current chunk, rows p = 16 pt + 4 g + jj, columns n = 16 nt + i
+  // running state: S_in of the current chunk in the accumulators' S^T
+  // layout, rows n = 16 nt + 4 g + jj, columns p = 16 pt + i (4 consecutive n
+  // of one p per lane)
   const int64_t PN = (int64_t)kP * N;
+  auto sidx = [&](int a, int n) __attribute__((always_inline)) { return (16 * (2 * pp + a) + i) * N + 16 * (nt0 + n) + 4 * g; };
   f32x4 st[2][NTW];
 #pragma unroll
   for (int a = 0; a < 2; ++a)
 #pragma unroll
     for (int n = 0; n < NTW; ++n)
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-        st[a][n][jj] = sp.init ? sp.init[bh * PN + (16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] : 0.f;
+      st[a][n] = sp.init ? *reinterpret_cast<const f32x4*>(sp.init + bh * PN + sidx(a, n)) : f32x4{0.f, 0.f, 0.f, 0.f};
   if constexpr (DB) {
     issue_chunk(0, 0);
     dma_wait();
     __syncthreads();
   }
 
+  // the chain's decays, 64 chunks at a time: lane k holds decay[c0 + k]
+  float decv = 0.f;
+  constexpr int kStores = 2 * NTW;  // S_in stores per lane and chunk
   for (int c = 0; c < p.nchunks; ++c) {
+    // decay[c] from the lanes' block, loaded (and waited for) before this
+    // chunk's copies are issued, so that wait does not include them
+    if ((c & 63) == 0) decv = c + lane < p.nchunks ? sp.decay[(int64_t)bh * p.nchunks + c + lane] : 0.f;
+    const float dec = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, decv), c & 63));
     // DB: the next chunk's copies run under this chunk's compute; otherwise
     // this chunk's copies are waited for here (other workgroups on the CU
-    // cover the latency)
+    // cover the latency).  S_in[c] -- the running state as the chunk begins
+    // -- is stored after the copies are issued, so the waits for the copies
+    // (vmcnt retires in issue order) leave the stores in flight.
     const int bf = DB ? (c & 1) : 0;
+    float* sg = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * PN;
     if constexpr (DB) {
       if (c + 1 < p.nchunks) issue_chunk(c + 1, bf ^ 1);
     } else {
       issue_chunk(c, 0);
-      dma_wait();
+    }
+#pragma unroll
+    for (int a = 0; a < 2; ++a)
+#pragma unroll
+      for (int n = 0; n < NTW; ++n) *reinterpret_cast<f32x4*>(sg + sidx(a, n)) = st[a][n];
+    if constexpr (!DB) {
+      vm_wait<kStores>();
       __syncthreads();
     }
-    const float dec = sp.decay[(int64_t)bh * p.nchunks + c];
     const float* xb = xs[bf];
     const float* bl = bs[bf];
     const float* ab = al[bf];
@@ -299,30 +318,24 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
 #pragma unroll
         for (int j = 0; j < 8; ++j) xf[j] = xb[swz_off(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)] * w[j];
 #pragma unroll
-        for (int n = 0; n < NTW; ++n) acc[a][n] = mma(xf, bfr[n], acc[a][n]);
+        for (int n = 0; n < NTW; ++n) acc[a][n] = mma(bfr[n], xf, acc[a][n]);
       }
     }
-    // S_in[c], then the recurrence (state_passing's f32 FMA)
-    float* sg = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * PN;
+    // the recurrence (state_passing's f32 FMA)
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int n = 0; n < NTW; ++n) {
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) sg[(16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] = st[a][n][jj];
-        st[a][n] = st[a][n] * dec + acc[a][n];
-      }
-    dma_wait();
+      for (int n = 0; n < NTW; ++n) st[a][n] = st[a][n] * dec + acc[a][n];
+    // DB: the next chunk's copies have landed (the stores may still be in
+    // flight); either way every wave is done with this chunk's buffer
+    if constexpr (DB) vm_wait<kStores>();
     __syncthreads();
   }
   if (sp.final_state) {
 #pragma unroll
     for (int a = 0; a < 2; ++a)
 #pragma unroll
-      for (int n = 0; n < NTW; ++n)
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj)
-          sp.final_state[bh * PN + (16 * (2 * pp + a) + 4 * g + jj) * N + 16 * (nt0 + n) + i] = st[a][n][jj];
+      for (int n = 0; n < NTW; ++n) *reinterpret_cast<f32x4*>(sp.final_state + bh * PN + sidx(a, n)) = st[a][n];
   }
 }
 
