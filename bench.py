@@ -57,15 +57,17 @@ def esize(dt):
     return torch.tensor([], dtype=dt).element_size()
 
 
-def kernel_model(cfg, state_dtype, handover=None):
+def kernel_model(cfg, state_dtype, handover=None, local_f16=False):
     """Algorithmic HBM bytes and MFMA flops per launch of each kernel.
 
     Bytes count every operand read once and every result written once at its
     storage type (B and C per group, not per head); the states entering each
     chunk at the format K3 hands them to K4 in (``handover`` "f16s": 2 bytes
     per state plus a 4-byte scale per state row; otherwise the state dtype,
-    the (hi, lo) pairs taking 4 bytes).  Flops count useful work: the causal
-    triangle T_Q = Q(Q+1)/2 of the intra-chunk products.
+    the (hi, lo) pairs taking 4 bytes); the local states between chunk_state
+    and state_passing at the state dtype, or (``local_f16``) as f16 with a
+    4-byte scale per row and 16-column tile.  Flops count useful work: the
+    causal triangle T_Q = Q(Q+1)/2 of the intra-chunk products.
     """
     b, L, h, P, N, Q, g = cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.chunk, cfg.ngroups
     c = L // Q
@@ -75,7 +77,7 @@ def kernel_model(cfg, state_dtype, handover=None):
     a = b * L * h * 4
     acs = b * h * c * Q * 4
     dec = b * h * c * 4
-    st = b * c * h * P * N * ss
+    st = b * c * h * (P * N * 2 + P * (N // 16) * 4) if local_f16 else b * c * h * P * N * ss
     sin = b * c * h * (P * N * 2 + P * 4) if handover == "f16s" else st
     fin = b * h * P * N * 4 if cfg.final_state else 0
     init = b * h * P * N * 4 if cfg.init_state else 0
@@ -92,6 +94,20 @@ def kernel_model(cfg, state_dtype, handover=None):
         "chunk_scan": dict(bytes=x + 2 * bc + acs + sin + x,
                            flops=b * c * h * (2 * TQ * N + 2 * TQ * P + 2 * Q * N * P)),
     }
+
+
+def takes_state_chain(cfg, split):
+    """ssd_forward's dispatch for K2 + K3 at chunk 256 with a hand-over format
+    (chunk_state_chain_plan in the library): one state-chain launch when the
+    (batch, head) chains keep every CU about equally busy (at least 3/4 of the
+    busiest CU's chains on the average CU) or number between one and two per
+    CU (d_state 128 for "f16s"); otherwise chunk_state then state_passing."""
+    if split is None or (split == "f16s" and cfg.dstate != 128):
+        return False
+    chains = cfg.batch * cfg.nheads
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    per_cu = -(-chains // cus)
+    return 4 * chains >= 3 * per_cu * cus or cus < chains < 2 * cus
 
 
 def end_to_end_model(cfg):
@@ -335,7 +351,12 @@ def main():
     split = None
     if prep is not None and state_dtype == torch.float32:
         split = cfg.dtype if args.state_format == "split" else "f16s"
-    S_in, _ = S.state_passing(states, decay, init, split=split)
+    # where the forward runs chunk_state then state_passing with the f16s
+    # hand-over, the local states cross HBM as f16 rows: time those variants
+    local_f16 = split == "f16s" and not takes_state_chain(cfg, split)
+    if local_f16:
+        states = S.chunk_state(X, B, Acs, state_dtype="f16s", prep=prep).states
+    S_in, _ = S.state_passing(S.F16SLocalStates(states) if local_f16 else states, decay, init, split=split)
     # K3 is timed in place on its own buffers, re-applying the recurrence to
     # their contents on every launch: the same traffic and instructions (nothing
     # in the kernel depends on the values, which stop being meaningful).  The
@@ -350,13 +371,13 @@ def main():
     def sp_launch():
         buf = sp_bufs[sp_next[0] % nbuf]
         sp_next[0] += 1
-        return S.state_passing_(buf, decay, init, sp_final, split=split, scales=sp_scales)
+        return S.state_passing_(buf, decay, init, sp_final, split=split, scales=sp_scales, f16_local=local_f16)
 
     sp_final = torch.empty(cfg.batch, cfg.nheads, cfg.headdim, cfg.dstate, device=dev) if cfg.final_state else None
     kfn = {
         "chunk_cumsum": lambda: S.chunk_cumsum(A, cfg.chunk),
         "chunk_prep": lambda: S.chunk_prep(B, C, cfg.chunk),
-        "chunk_state": lambda: S.chunk_state(X, B, Acs, state_dtype=state_dtype, prep=prep),
+        "chunk_state": lambda: S.chunk_state(X, B, Acs, state_dtype="f16s" if local_f16 else state_dtype, prep=prep),
         "state_passing": sp_launch,
         "chunk_state_passing": lambda: S.chunk_state_passing(X, B, Acs, decay, prep=prep, initial_states=init,
                                                              return_final_states=cfg.final_state, split=split,
@@ -366,7 +387,7 @@ def main():
     }
     if prep is None:
         del kfn["chunk_prep"]
-    model = kernel_model(cfg, state_dtype, split if isinstance(split, str) else None)
+    model = kernel_model(cfg, state_dtype, split if isinstance(split, str) else None, local_f16)
     kernels = {}
     for name, fn in kfn.items():
         fn()
@@ -414,6 +435,8 @@ def main():
                    "dstate": cfg.dstate, "chunk": cfg.chunk, "ngroups": cfg.ngroups,
                    "inputs": f"{DTYPE_NAMES[cfg.dtype]} X/B/C, f32 A", "state_storage": args.state_dtype,
                    "state_handover": split if isinstance(split, str) else ("split" if split is not None else None),
+                   "local_states": ("f16 rows" if local_f16 else
+                                    "in registers (state chain)" if takes_state_chain(cfg, split) else args.state_dtype),
                    "final_state": cfg.final_state, "initial_state": cfg.init_state},
         "device_ms_per_step": round(dev_ms, 5),
         "step_stats": stats,

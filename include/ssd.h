@@ -41,10 +41,10 @@
 extern "C" {
 #endif
 
-#define SSD_ABI_VERSION 5
+#define SSD_ABI_VERSION 6
 
 /* Element types.  The SPLIT and F16S values are storage formats of the
- * per-chunk states only, both laid out in the f32 states buffer
+ * per-chunk states only, all laid out in the f32 states buffer
  * [b, c, h, P, N] (4 bytes per state):
  *   SPLIT: each f32 state as the 16-bit pair hi = round(v), lo = round(v - hi)
  *     of the inputs' type, stored per 8 consecutive states as [hi x8 | lo x8].
@@ -53,12 +53,20 @@ extern "C" {
  *     state_scales [b, c, h, P]; e is chosen per row so that the row's largest
  *     |v| lies in [2^14, 2^15] (f16's 11-bit significand; MR:155 itself stores
  *     the states in float16).
- * ssd_state_passing and ssd_chunk_state_passing write them from f32 local
- * states; ssd_chunk_scan reads them, for 16-bit inputs at chunk 256 and
- * dstate 64 / 128 (F16S with dstate 128 for the one-launch state chain), as
- * MFMA operands without converting them.  ssd_forward hands the states to
- * chunk_scan as F16S wherever that applies (state_dtype SSD_DTYPE_F32), or
- * in the format state_dtype names. */
+ *   F16S_LOCAL: the local states (K2's output) as f16 values in the first
+ *     halves of the rows, as F16S, but with a scale 2^e per row p and
+ *     16-column tile t (the tile row's largest |v| in [2^14, 2^15]) kept in
+ *     the states buffer: the P x N/16 scales of an item [P][N], in (p, t)
+ *     order k = p N/16 + t, packed into the second halves (unused by the f16
+ *     values) of its first rows, scale k as the f32 in slot N/2 + k % (N/2)
+ *     of row k / (N/2).
+ * ssd_state_passing and ssd_chunk_state_passing write SPLIT and F16S from f32
+ * (or F16S_LOCAL) local states; ssd_chunk_scan reads them, for 16-bit inputs
+ * at chunk 256 and dstate 64 / 128 (F16S with dstate 128 for the one-launch
+ * state chain), as MFMA operands without converting them.  ssd_chunk_state
+ * writes F16S_LOCAL for 16-bit inputs at chunk 256 and dstate 64 / 128.
+ * ssd_forward hands the states to chunk_scan as F16S wherever that applies
+ * (state_dtype SSD_DTYPE_F32), or in the format state_dtype names. */
 enum {
   SSD_DTYPE_F32 = 0,
   SSD_DTYPE_BF16 = 1,
@@ -66,6 +74,7 @@ enum {
   SSD_STATE_SPLIT_BF16 = 3,
   SSD_STATE_SPLIT_F16 = 4,
   SSD_STATE_F16S = 5,
+  SSD_STATE_F16S_LOCAL = 6,
 };
 
 /* Status codes (negative: rejected on the host before any launch). */
@@ -139,6 +148,9 @@ int ssd_chunk_prep(const ssd_dims* d, int dtype,
  *   states[b,c,h,p,n] = sum_l x[l,p] dt[l] exp(Acs[Q-1]-Acs[l]) bmat[l,n].
  * Replaces MR:144 (X*dt) and MR:148-149 (decay_to_end and the 3-operand
  * einsum).  MR's [.., N, P] state is stored here as [.., P, N].
+ * state_dtype: SSD_DTYPE_F32 / BF16, or SSD_STATE_F16S_LOCAL (16-bit inputs at
+ * chunk 256, dstate 64 / 128; the f32 local states rounded to f16 rows with
+ * their row scale, for ssd_state_passing with SSD_STATE_F16S_LOCAL).
  * prep: NULL, or ssd_chunk_prep's output for the same d, dtype and bmat. */
 int ssd_chunk_state(const ssd_dims* d, int dtype,
                     const void* x, const int64_t x_strides[4],
@@ -153,20 +165,29 @@ int ssd_chunk_state(const ssd_dims* d, int dtype,
  * Replaces the Python loop at MR:152-157.  final_states (optional) receives
  * the state after the last chunk, which MR computes and discards (MR:156).
  * state_scales: [b, c, h, P] f32, written for SSD_STATE_F16S (NULL otherwise);
- * the same argument of ssd_chunk_state_passing and ssd_chunk_scan. */
+ * the same argument of ssd_chunk_state_passing and ssd_chunk_scan.
+ * state_dtype names S_in's format; the local states are f32 for the SPLIT
+ * formats and F16S, else of state_dtype.  SSD_STATE_F16S_LOCAL: the local
+ * states in that format (ssd_chunk_state's), S_in written as SSD_STATE_F16S
+ * with state_scales (dstate 64 / 128). */
 int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, float* state_scales,
                       const float* chunk_decay, const float* initial_states,
                       float* final_states, void* stream);
 
 /* K2 then K3 as ssd_forward runs them: on return states holds S_in (the
  * state entering each chunk, [b, c, h, P, N]) in state_dtype, exactly as
- * ssd_chunk_state (f32 local states for the SPLIT formats, else state_dtype)
- * followed by ssd_state_passing would leave it.  For a SPLIT state_dtype of
- * the inputs' type with prep (chunk 256), and for f32 inputs with f32 states
- * at chunk 64 / 128 and dstate 64 / 128 (chunk x dstate <= 8192), the two
- * stages run as one launch (for SPLIT, wherever that is faster on the
- * device): each (b, h) chain of chunks keeps its running state in registers
- * and the local states are never stored.
+ * ssd_chunk_state (f32 local states for the SPLIT formats and F16S, else
+ * state_dtype) followed by ssd_state_passing would leave it.  For a SPLIT
+ * state_dtype of the inputs' type or F16S with prep (chunk 256), and for f32
+ * inputs with f32 states at chunk 64 / 128 and dstate 64 / 128 (chunk x
+ * dstate <= 8192), the two stages run as one launch (for SPLIT and F16S,
+ * wherever that is faster on the device): each (b, h) chain of chunks keeps
+ * its running state in registers and the local states are never stored.
+ * Where F16S's two stages run as separate launches (16-bit inputs at chunk
+ * 256) they pass the local states as SSD_STATE_F16S_LOCAL, half the bytes of
+ * f32: the result is then that of ssd_chunk_state with SSD_STATE_F16S_LOCAL
+ * followed by ssd_state_passing with SSD_STATE_F16S_LOCAL, and differs from
+ * the one-launch result by the local states' f16 rounding.
  * Replaces MR:144-157 (X*dt, decay_to_end, block_state, the state loop).
  * a_cumsum, chunk_decay: ssd_chunk_cumsum's outputs; prep as for
  * ssd_chunk_state; initial_states / final_states as for ssd_state_passing. */

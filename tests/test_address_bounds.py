@@ -66,6 +66,13 @@ def inside(name, idx, lo, hi):
     assert lo <= mn and mx < hi, f"{name}: touches [{mn}, {mx}], allowed [{lo}, {hi})"
 
 
+def f16l_scale_slot(p, t, N):
+    """ssd_device.h f16l_scale_slot: the item slot of the scale of row p's n tile t."""
+    pin("ssd_device.h", "const int k = p * (N / 16) + t;", "return (k / (N / 2)) * N + N / 2 + k % (N / 2);")
+    k = p * (N // 16) + t
+    return (k // (N // 2)) * N + N // 2 + k % (N // 2)
+
+
 def lanes():
     """(wave, lane) grids of an 8-wave workgroup, shapes [8, 1] and [1, 64]."""
     return np.arange(8)[:, None], np.arange(64)[None, :]
@@ -249,7 +256,9 @@ def test_chunk_state_q256_and_chain_addresses(name):
         "bh = plan.nfull + sg / plan.seg_per_chain;",
         "c0 = (sg % plan.seg_per_chain) * plan.seg_len;",
         "c1 = min(c0 + plan.seg_len, p.nchunks);",
-        "if (c0 >= c1) return;  // the whole workgroup, before any barrier")
+        "if (c0 >= c1) return;  // the whole workgroup, before any barrier",
+        "*reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;",
+        "if (g == 0) item[f16l_scale_slot<N>(row, nt)] = __builtin_ldexpf(1.f, e);")
     wave, lane = lanes()
     g, i = lane >> 4, lane & 15
     nt, pt0 = wave % NT, (wave // NT) * PTW
@@ -259,6 +268,15 @@ def test_chunk_state_q256_and_chain_addresses(name):
     inside("state columns", 16 * nt + 4 * g + 3, 0, N)
     inside("f16s: f16 columns in the row's first half", 16 * nt + 4 * g + 3, 0, N)
     inside("f16s scales rows", 16 * (pt0 + q) + i, 0, P)
+    # K2's f16 local states: f16 columns in the row's first half, the tile
+    # scales packed into the second halves of the item's first rows (every
+    # (row, tile)'s slot distinct, none in an f16 half)
+    inside("f16 local: f16 slots (f32 units)", (16 * nt + 4 * g + 3) // 2, 0, N // 2)
+    pp_, tt_ = np.meshgrid(np.arange(P), np.arange(NT), indexing="ij")
+    slot = f16l_scale_slot(pp_, tt_, N)
+    inside("f16 local: scale slots in the item", slot, 0, P * N)
+    assert len(set(slot.ravel().tolist())) == P * NT and ((slot % N) >= N // 2).all()
+    inside("f16 local: the store's tile", nt, 0, NT)
     # x copy parts, Acs, dt: as chunk_scan's (8-row blocks blk = wave + 8 m, m < 4)
     blk = wave + 8 * np.arange(4)[:, None, None]
     inside("x rows in the chunk", 8 * blk + (lane >> 3), 0, Q)
@@ -481,7 +499,10 @@ def test_state_passing_addresses(name):
         "float* elem = base + SPT * (int64_t)v;",
         "*reinterpret_cast<H*>(hrow + c * 2 * cstride) = hv;",
         "constexpr int spt = 4;",
-        "const int c = min(c0 + u, nchunks - 1);")
+        "const int c = min(c0 + u, nchunks - 1);",
+        "const float* rscale = base + f16l_scale_slot<N>(row, col / 16);",
+        "const H* q = reinterpret_cast<const H*>(hrow + c * 2 * cstride);",
+        "const float sc = rscale[c * cstride];")
     PN = P * N
     nc = L // Q
     chains = B * H
@@ -499,6 +520,9 @@ def test_state_passing_addresses(name):
             row, col = v // tpr, per_thread * (v % tpr)
             inside("f16s rows", row, 0, P)
             inside("f16s f16 columns (the row's first half)", col + per_thread - 1, 0, N)
+            # f16 local states in: the same f16 slots, and the row's packed scale
+            inside("f16 local scale slot", f16l_scale_slot(row, col // 16, N), 0, PN)
+            assert ((col + per_thread - 1) // 16 == col // 16).all()
     # the chunk index every (clamped) load of the pipelined chain uses (batches of 4 or 8)
     for unroll in (4, 8):
         for nchunks in sorted({1, 2, 7, 16, 17, nc}):

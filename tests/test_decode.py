@@ -3,7 +3,10 @@ the float64 sequential-scan oracle (oracle/ssd_oracle.py ``ssd_sequential``,
 the per-token form of workloads/mamba/model_ref.py:152-161).
 
 Tolerances: f32 1e-4; 16-bit inputs 2e-2 (y is rounded to the input type;
-the state stays f32 and is held to 1e-4 relative to its scale)."""
+the state stays f32 and is held to 1e-4 relative to its scale, or 2e-3 where
+the forward that produced it passed its local states as f16 rows: chunk 256
+without the state chain, half an f16 ulp of each row's largest local
+state)."""
 
 import numpy as np
 import pytest
@@ -11,6 +14,7 @@ import torch
 
 from oracle import layer_oracle as LO
 from oracle import ssd_oracle as O
+from state_plans import f16_local
 from workloadsuite_amd import ssd as S
 from workloadsuite_amd.configs import tolerance
 
@@ -138,4 +142,5 @@ def test_decode_several_steps_after_forward(k, dtype, Q, N, g, h, b):
         y = S.decode_step(state, d(X[:, s]), d(B[:, s]), d(C[:, s]), d(A[:, s]), dt=d(dt[:, s]))
         close(y, Ys[:, s], tolerance(dtype))
     scale = float(np.abs(fs).max())
-    close(state / scale, fs / scale, 1e-4)
+    f16l = dtype != torch.float32 and Q == 256 and N in (64, 128) and f16_local(b * h, N)
+    close(state / scale, fs / scale, 2e-3 if f16l else 1e-4)

@@ -23,6 +23,7 @@ import torch
 
 from oracle import ssd_oracle as O
 from parity_bounds import check_within, f32_reference_bounds
+from state_plans import f16_local, k2_k3_f16s
 from workloadsuite_amd import ssd as S
 from workloadsuite_amd.configs import CONFIGS, make_inputs, tolerance
 from workloadsuite_amd.mamba_ssd import build_workload
@@ -135,6 +136,76 @@ def test_k3_f16s_format(N, init):
     assert ((dec - r).abs() <= sc[..., None] * 2.0 ** 3 * (1 + 1e-9)).all()   # half an f16 ulp at 2^14..2^15
 
 
+def _check_f16_rows(v, sc, ref):
+    """f16 row values v [.., R, M] with power-of-two row scales sc [.., R]:
+    row maxima in [2^14, 2^15] and v sc within half an f16 ulp of the row's
+    scale of the f32 reference."""
+    assert torch.equal(torch.exp2(torch.log2(sc).round()), sc)   # powers of two
+    vmax = v.abs().amax(-1)
+    live = vmax > 0
+    # (a row maximum just below 2^15 may round up to it)
+    bad = live & ~((vmax >= 2.0 ** 14) & (vmax <= 2.0 ** 15))
+    assert not bad.any(), f"row maxima outside [2^14, 2^15]: {vmax[bad][:8].tolist()} scales {sc[bad][:8].tolist()}"
+    assert ((v * sc[..., None] - ref).abs() <= sc[..., None] * 2.0 ** 3 * (1 + 1e-9)).all()
+
+
+def _f16_local_case(dtype, N, nc, h=40, g=2, seed=3):
+    """Inputs at chunk 256 whose local state rows span 6 decades (x scaled per
+    column p), with dt; 2 * nc * h items, more than the CUs for nc >= 4."""
+    cfg, inp = small_case(dtype, 256, N, b=2, nc=nc, h=h, g=g, seed=seed)
+    d = to_dev(inp)
+    col = torch.logspace(-3, 3, 64, device=DEV).to(dtype)
+    X = (d["X"] * col).contiguous()
+    dt = torch.rand(2, nc * 256, h, generator=torch.Generator().manual_seed(seed)).to(DEV) + 0.5
+    Acs, dec = S.chunk_cumsum(d["A"], 256)
+    return X, d["B"], d["C"], Acs, dec, dt
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("N", [64, 128])
+def test_k2_f16s_local_format(dtype, N):
+    """chunk_state(..., state_dtype="f16s") at chunk 256: row p of each local
+    state holds N f16 values v in the first half of its f32 slots, and the
+    item's packed scales a power of two s per row and 16-column tile with
+    max|v| over the tile row in [2^14, 2^15]; v s is chunk_state's f32 local
+    state to within half an f16 ulp of the tile's scale.  With and without
+    chunk_prep's operands and dt."""
+    say("k2 f16s local", dtype, N)
+    X, B, C, Acs, _, dt = _f16_local_case(dtype, N, nc=5)
+    prep = S.chunk_prep(B, C, 256)
+    for pr in (None, prep):
+        for dtv in (None, dt):
+            ref = S.chunk_state(X, B, Acs, dt=dtv, prep=pr)
+            got = S.chunk_state(X, B, Acs, dt=dtv, prep=pr, state_dtype="f16s")
+            assert isinstance(got, S.F16SLocalStates)
+            torch.cuda.synchronize()
+            v = got.states.view(torch.float16)[..., :N].double().cpu()
+            sc = got.scales().double().cpu()
+            tiles = lambda t: t.unflatten(-1, (N // 16, 16))  # noqa: E731  [.., P, N/16, 16]
+            _check_f16_rows(tiles(v), sc, tiles(ref.double().cpu()))
+            assert torch.allclose(got.decode().double().cpu(), v * sc.repeat_interleave(16, -1))
+
+
+@pytest.mark.parametrize("N", [64, 128])
+@pytest.mark.parametrize("nc,init", [(5, False), (12, True), (3, True)])
+def test_k3_f16s_local_input(N, nc, init):
+    """state_passing on f16 local states (chunk_state's "f16s") gives bit for
+    bit what it gives on their f32 values, which f16 value times a power of two
+    is exactly: S_in as "f16s" and the final state (chains of 3, 5, 12 chunks:
+    both load paths)."""
+    say("k3 f16s local", N, nc, init)
+    X, B, C, Acs, dec, dt = _f16_local_case(torch.bfloat16, N, nc=nc, h=6, g=3)
+    loc = S.chunk_state(X, B, Acs, dt=dt, state_dtype="f16s")
+    s0 = torch.randn(2, 6, 64, N, generator=torch.Generator().manual_seed(nc)).to(DEV) if init else None
+    got, fin = S.state_passing(loc, dec, s0, split="f16s")
+    ref, rfin = S.state_passing(loc.decode(), dec, s0, split="f16s")
+    torch.cuda.synchronize()
+    assert torch.equal(fin, rfin)
+    assert torch.equal(got.scales, ref.scales)
+    assert torch.equal(got.states.view(torch.float16)[..., :N], ref.states.view(torch.float16)[..., :N])
+    assert torch.equal(loc.scales(), S.chunk_state(X, B, Acs, dt=dt, state_dtype="f16s").scales())
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("Q", [64, 128, 256])
 @pytest.mark.parametrize("N", [16, 32, 64, 128])
@@ -242,9 +313,12 @@ def test_forward_equals_kernel_by_kernel(dtype, N, h, g, use_dt):
     # the forward's own K3 -> K4 hand-over: S_in stored as (hi, lo) pairs
     S_sp, fin_sp = S.state_passing(st, dec, split=dtype)
     Ys = S.chunk_scan(d["X"], d["B"], d["C"], Acs, S_sp, dt=dt, prep=prep, split=True)
-    # the default forward hands S_in over as f16 rows with per-row scales
+    # the default forward hands S_in over as f16 rows with per-row scales (and
+    # here, with chunk_state and state_passing as separate launches, passes
+    # the local states as f16 rows too)
+    assert f16_local(4 * h, N)
     Yf, final_f = S.ssd_forward(d["X"], d["A"], d["B"], d["C"], 256, dt=dt, return_final_states=True)
-    S_f, fin_f = S.state_passing(st, dec, split="f16s")
+    S_f, fin_f = k2_k3_f16s(d["X"], d["B"], Acs, dec, dt=dt, prep=prep)
     Yfk = S.chunk_scan(d["X"], d["B"], d["C"], Acs, S_f, dt=dt, prep=prep, split="f16s")
     torch.cuda.synchronize()
     assert torch.equal(Y, Yk)
@@ -253,7 +327,7 @@ def test_forward_equals_kernel_by_kernel(dtype, N, h, g, use_dt):
     assert torch.equal(final, fin)
     assert torch.equal(fin_sp, fin)
     assert torch.equal(Yf, Yfk)
-    assert torch.equal(final_f, fin) and torch.equal(fin_f, fin)
+    assert torch.equal(final_f, fin_f)
 
 
 # ---------------------------------------------------------------------------

@@ -18,6 +18,7 @@ import torch
 
 from oracle import layer_oracle as LO
 from oracle import ssd_oracle as O
+from state_plans import k2_k3_f16s
 from workloadsuite_amd import ssd as S
 from workloadsuite_amd.configs import tolerance
 
@@ -196,9 +197,10 @@ def test_ssd_layer_equals_its_kernels_one_by_one(dtype, N, g, h):
     y = S.ssd_layer(x, z, B, C, dt, dev["conv_w"], dev["conv_b"], dev["dt_bias"], dev["A_log"], dev["D"], 64, h)
     X, dto, Acs, dec = S.layer_prep(x, dt, dev["conv_w"], dev["conv_b"], dev["dt_bias"], dev["A_log"], Q, h)
     prep = S.chunk_prep(B, C, Q)
-    st = S.chunk_state(X, B, Acs, dt=dto, prep=prep)
-    # the layer hands S_in to chunk_scan as f16 rows with per-row scales
-    S_in, _ = S.state_passing(st, dec, split="f16s")
+    # the layer hands S_in to chunk_scan as f16 rows with per-row scales (the
+    # local states as f16 rows too where chunk_state and state_passing run as
+    # separate launches)
+    S_in, _ = k2_k3_f16s(X, B, Acs, dec, dt=dto, prep=prep)
     yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dto, prep=prep, split="f16s", D=dev["D"], z=z.reshape(b, L, h, P))
     torch.cuda.synchronize()
     assert torch.equal(y, yk.reshape(b, L, h * P))

@@ -17,25 +17,12 @@ The per-kernel path itself is held to the oracle by the parity tests."""
 import pytest
 import torch
 
+from state_plans import chain_plan, k2_k3_f16s
 from workloadsuite_amd import ssd as S
 
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-
-
-def chain_plan(chains):
-    """The library's dispatch rule (chunk_state_chain_plan) on this device:
-    "whole" (every chain in one workgroup), "mixed" (one whole chain per CU,
-    the rest in segments finished by state_passing) or None (chunk_state then
-    state_passing)."""
-    cus = torch.cuda.get_device_properties(0).multi_processor_count
-    per_cu = -(-chains // cus)
-    if 4 * chains >= 3 * per_cu * cus:
-        return "whole"
-    if cus < chains < 2 * cus:
-        return "mixed"
-    return None
 
 
 def takes_chain(chains):
@@ -49,8 +36,13 @@ def kernels_one_by_one(X, A, B, C, dt, init, fmt, Q=256):
     """K1, K0, K2, K3 (handing S_in over in `fmt`), K4 through their own entry points."""
     Acs, decay = S.chunk_cumsum(A, Q)
     prep = S.chunk_prep(B, C, Q)
-    st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
-    S_in, fk = S.state_passing(st, decay, initial_states=init, split=X.dtype if fmt == "split" else "f16s")
+    if fmt == "f16s":
+        # f32 local states where the forward runs the state chain, f16 rows
+        # where it runs chunk_state then state_passing (d_state 64 here)
+        S_in, fk = k2_k3_f16s(X, B, Acs, decay, dt=dt, prep=prep, initial_states=init)
+    else:
+        st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
+        S_in, fk = S.state_passing(st, decay, initial_states=init, split=X.dtype)
     Yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dt, prep=prep, split=True if fmt == "split" else "f16s")
     return Yk, fk
 
@@ -137,14 +129,20 @@ def test_mixed_plan_equals_kernels_one_by_one(dtype, b, h, L, g, fmt):
 def test_chunk_state_passing_entry_point(b, h, L, split):
     """ssd_chunk_state_passing (whole chains, the mixed plan, or chunk_state
     then state_passing, by shape) against the two entry points it stands for,
-    bit for bit; also without split (f32 S_in, always two launches)."""
+    bit for bit (with f16 local states for "f16s" where the two run as
+    separate launches); also without split (f32 S_in, always two launches)."""
     print("CASE chunk_state_passing", b, h, L, split, flush=True)
     X, A, B, C, dt, init = case(torch.bfloat16, b, L, h, 64, 128, 2, seed=h + L)
     Acs, decay = S.chunk_cumsum(A, 256)
     prep = S.chunk_prep(B, C, 256)
     S_in, final = S.chunk_state_passing(X, B, Acs, decay, dt=dt, prep=prep, initial_states=init, split=split)
-    st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
-    S_ref, f_ref = S.state_passing(st, decay, initial_states=init, split=split)
+    if split == "f16s":
+        # the local states as the forward passes them at this shape (f16 rows
+        # where chunk_state then state_passing run)
+        S_ref, f_ref = k2_k3_f16s(X, B, Acs, decay, dt=dt, prep=prep, initial_states=init)
+    else:
+        st = S.chunk_state(X, B, Acs, dt=dt, prep=prep)
+        S_ref, f_ref = S.state_passing(st, decay, initial_states=init, split=split)
     torch.cuda.synchronize()
     assert torch.equal(final, f_ref)
     fmt = "f16s" if split == "f16s" else "split"

@@ -3,13 +3,22 @@ is a device array the library keeps per device) against ssd_forward with a
 caller-allocated workspace: the same kernels, so the same bits.  Two calls in
 a row, the second smaller; a call whose workspace exceeds the array (run in
 batch slices); an f32 call on the generic kernels; and a shape whose single
-batch element does not fit, rejected on the host before any launch."""
+batch element does not fit, rejected on the host before any launch.
+
+A batch slice has fewer (batch, head) chains than the whole call, and at
+chunk 256 the chain count picks how K2 + K3 run: one state-chain launch with
+f32 local states, or chunk_state then state_passing with the local states as
+f16 rows (the "f16s" hand-over).  Batch elements whose slice runs the other
+form than the whole call differ from it by the local states' f16 rounding:
+those are held to the bf16 tolerance (2e-2) and their final state to 2e-3 of
+its scale; every other batch element bit for bit."""
 
 import ctypes
 
 import pytest
 import torch
 
+from state_plans import f16_local
 from workloadsuite_amd import _lib
 from workloadsuite_amd import ssd as S
 from workloadsuite_amd.configs import CONFIGS, make_inputs
@@ -42,13 +51,31 @@ def test_noalloc_matches_forward_two_calls_second_smaller():
         assert torch.equal(Y1, Y0) and torch.equal(f1, f0)
 
 
+def noalloc_slices(cfg):
+    """ssd_forward_noalloc's batch slices: the largest slice whose workspace
+    fits the array, then the rest."""
+    ws = lambda b: S.workspace_bytes(b, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, cfg.chunk)  # noqa: E731
+    size = cfg.batch
+    while ws(size) > SCRATCH:
+        size -= 1
+    return [(b0, min(size, cfg.batch - b0)) for b0 in range(0, cfg.batch, size)]
+
+
 def test_noalloc_runs_batch_slices_when_the_workspace_exceeds_the_array():
     cfg = CONFIGS["C3"].scaled(batch=6, seqlen=4096)
     ws = S.workspace_bytes(cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, cfg.chunk)
     print("CASE noalloc slices", cfg, ws, flush=True)
     assert ws > SCRATCH
     Y0, f0, Y1, f1 = run_both(cfg, 2)
-    assert torch.equal(Y1, Y0) and torch.equal(f1, f0)
+    whole = f16_local(cfg.batch * cfg.nheads, cfg.dstate)
+    for b0, n in noalloc_slices(cfg):
+        sl = slice(b0, b0 + n)
+        if f16_local(n * cfg.nheads, cfg.dstate) == whole:
+            assert torch.equal(Y1[sl], Y0[sl]) and torch.equal(f1[sl], f0[sl])
+        else:
+            torch.testing.assert_close(Y1[sl].float(), Y0[sl].float(), rtol=2e-2, atol=2e-2)
+            scale = float(f0[sl].abs().max())
+            torch.testing.assert_close(f1[sl] / scale, f0[sl] / scale, rtol=2e-3, atol=2e-3)
 
 
 def test_noalloc_f32_generic_kernels():

@@ -291,7 +291,8 @@ CumsumArgs make_cumsum_args(const ssd_dims* d, const float* a, const int64_t a_s
 // K1 (when k1 is given; together with K0 in one launch where K0 applies), K0,
 // K2, K3, K4 of one forward.  Without k1, K1's outputs are already in the
 // workspace.  Operands are validated by the caller.
-// K2 then K3 (local states in the f32 / bf16 state_dtype; pa.split_dtype set:
+// K2 then K3 (local states in the f32 / bf16 state_dtype, or as f16 rows
+// where K3 writes F16S from the chunk-256 K2's output; pa.split_dtype set:
 // S_in written as hi/lo pairs), as one chain launch where that is faster.
 int run_state_passing(const ssd_dims* d, int dtype, const ChunkStateArgs& sa, const StatePassingArgs& pa,
                       int state_dtype, hipStream_t s) {
@@ -314,6 +315,13 @@ int run_state_passing(const ssd_dims* d, int dtype, const ChunkStateArgs& sa, co
       if ((rc = hip_status(ssd::launch_state_passing(rest, state_dtype, s)))) return rc;
     }
     return SSD_OK;
+  }
+  if (pa.f16s && ssd::chunk_state_persistent_supported(sa, dtype)) {
+    // S_in goes to chunk_scan as f16 rows: the local states cross HBM as f16
+    // rows too (SSD_STATE_F16S_LOCAL, half the bytes of f32 in K2's writes
+    // and K3's reads)
+    if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, SSD_STATE_F16S_LOCAL, s)))) return rc;
+    return hip_status(ssd::launch_state_passing(pa, SSD_STATE_F16S_LOCAL, s));
   }
   if ((rc = hip_status(ssd::launch_chunk_state(sa, dtype, state_dtype, s)))) return rc;
   return hip_status(ssd::launch_state_passing(pa, state_dtype, s));
@@ -576,7 +584,8 @@ int ssd_chunk_state(const ssd_dims* d, int dtype, const void* x, const int64_t x
                     int state_dtype, const void* prep, void* stream) {
   int rc = check_dims_impl(d, dtype);
   if (rc) return rc;
-  if (!valid_state_dtype(dtype, state_dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+  const bool f16l = state_dtype == SSD_STATE_F16S_LOCAL;
+  if (!valid_state_dtype(dtype, state_dtype) && !f16l) return SSD_ERR_UNSUPPORTED_DTYPE;
   if ((rc = check_vec_operand(x, x_strides, 4, dtype))) return rc;
   if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
@@ -584,6 +593,8 @@ int ssd_chunk_state(const ssd_dims* d, int dtype, const void* x, const int64_t x
   if (!aligned16(states)) return SSD_ERR_MISALIGNED;
   if (prep && (reinterpret_cast<uintptr_t>(prep) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
   ChunkStateArgs p = make_state_args(d, x, x_strides, bmat, b_strides, dt, dt_strides, a_cumsum, states);
+  // f16 local states: the chunk-256 kernel for 16-bit inputs only
+  if (f16l && !ssd::chunk_state_persistent_supported(p, dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
   if (prep_applies(d, dtype)) p.btf = prep_btf(d, prep);
   return hip_status(ssd::launch_chunk_state(p, dtype, state_dtype, (hipStream_t)stream));
 }
@@ -593,7 +604,8 @@ int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, float* s
   int rc = check_dims_impl(d, SSD_DTYPE_BF16);
   if (rc) return rc;
   const int split = split_of(state_dtype);
-  const bool f16s = state_dtype == SSD_STATE_F16S;
+  const bool f16l = state_dtype == SSD_STATE_F16S_LOCAL;  // F16S_LOCAL in, F16S out
+  const bool f16s = state_dtype == SSD_STATE_F16S || f16l;
   if (state_dtype != SSD_DTYPE_F32 && state_dtype != SSD_DTYPE_BF16 && !split && !f16s)
     return SSD_ERR_UNSUPPORTED_DTYPE;
   if (f16s && d->dstate != 64 && d->dstate != 128) return SSD_ERR_UNSUPPORTED_DSTATE;
@@ -606,7 +618,7 @@ int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, float* s
   p.split_dtype = split;
   p.f16s = f16s ? 1 : 0;
   p.sscale = f16s ? state_scales : nullptr;
-  return hip_status(ssd::launch_state_passing(p, f32_layout(state_dtype) ? SSD_DTYPE_F32 : state_dtype,
+  return hip_status(ssd::launch_state_passing(p, f16l ? SSD_STATE_F16S_LOCAL : f32_layout(state_dtype) ? SSD_DTYPE_F32 : state_dtype,
                                               (hipStream_t)stream));
 }
 

@@ -25,7 +25,17 @@
 //
 // Traffic per item: x 32 KB + Acs 1 KB read, states 32 KB (f32) written; B
 // once per group.  HBM bound at this shape.
+//
+// F16L (SSD_STATE_F16S_LOCAL): the 16 states of row p in n tile t are stored
+// as f16 values v / 2^e in the first half of the row's f32 slots, e chosen
+// per (p, t) so that the tile row's largest |v| lies in [2^14, 2^15], and the
+// item's P x N/16 scales 2^e (f32) packed into the second halves of its
+// first rows -- 18 KB written per item instead of 32 KB, in whole cache lines
+// (MR:148-149 itself forms the states in the inputs' 16-bit type and MR:155
+// stores them in float16).  A tile row lies in one wave (lanes i, i + 16,
+// i + 32, i + 48 hold its 16 states), so its maximum takes two lane swaps.
 #include <climits>
+#include <type_traits>
 
 #include "ssd_device.h"
 #include "ssd_launch.h"
@@ -69,12 +79,13 @@ template <> struct StateStore<bf16> {
 };
 
 
-template <typename T, typename S, int NK, bool HAS_DT, bool PREP>
+template <typename T, typename S, int NK, bool HAS_DT, bool PREP, bool F16L>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void chunk_state_q256_kernel(ChunkStateArgs p) {
   constexpr int N = 32 * NK;        // dstate (64 or 128)
   constexpr int NTILE = N / 16;     // n tiles
   constexpr int PTW = NTILE / 2;    // p tiles per wave (4 for N=128, 2 for N=64)
+  static_assert(!F16L || std::is_same<S, float>::value, "f16 local states live in the f32 layout");
   // [half][buffer]: each half's current item and its next one (in flight)
   __shared__ __attribute__((aligned(1024))) T xr[kHalves][2][kQ * kP];
   __shared__ __attribute__((aligned(16))) float ar[kHalves][2][kQ];
@@ -199,7 +210,26 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
   f32x4 st_prev[PTW];
   auto store_state = [&](const Item& r, int q) __attribute__((always_inline)) {
     S* sg = reinterpret_cast<S*>(p.states) + (((int64_t)r.b * p.nchunks + r.c) * p.nheads + r.h) * (int64_t)(kP * N);
-    StateStore<S>::store(sg + srow + 16 * N * q, st_prev[q]);
+    if constexpr (F16L) {
+      // the largest |state| of row 16 (pt0 + q) + i in this wave's n tile:
+      // swap with the neighbouring 16-lane row, then with the other 32-lane half
+      const f32x4 v = st_prev[q];
+      float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+      m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+      m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+      const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
+      f16x4 hv;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) hv[k] = (f16)__builtin_ldexpf(v[k], -e);
+      const int row = 16 * (pt0 + q) + i;
+      float* item = reinterpret_cast<float*>(sg);
+      *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;
+      if (g == 0) item[f16l_scale_slot<N>(row, nt)] = __builtin_ldexpf(1.f, e);
+    } else {
+      StateStore<S>::store(sg + srow + 16 * N * q, st_prev[q]);
+    }
   };
 
   // The two halves take alternate items of the range (half h: it0 + h,
@@ -240,7 +270,8 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
       prev = cur;
     }
     // the next item's copy, issued before this step's PTW state stores, must
-    // have landed; the stores may still be in flight
+    // have landed; the stores may still be in flight (F16L: PTW more stores of
+    // the tile scales, part of which this wait then covers)
     if (active && has_prev) vm_wait<PTW>();
     else dma_wait();
     __syncthreads();
@@ -262,21 +293,21 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
   }
 }
 
-template <typename T, typename S, int NK>
+template <typename T, typename S, int NK, bool F16L = false>
 hipError_t launch_nk(const ChunkStateArgs& a, hipStream_t stream) {
-  auto kern = a.dt ? (a.btf ? chunk_state_q256_kernel<T, S, NK, true, true> : chunk_state_q256_kernel<T, S, NK, true, false>)
-                   : (a.btf ? chunk_state_q256_kernel<T, S, NK, false, true> : chunk_state_q256_kernel<T, S, NK, false, false>);
+  auto kern = a.dt ? (a.btf ? chunk_state_q256_kernel<T, S, NK, true, true, F16L> : chunk_state_q256_kernel<T, S, NK, true, false, F16L>)
+                   : (a.btf ? chunk_state_q256_kernel<T, S, NK, false, true, F16L> : chunk_state_q256_kernel<T, S, NK, false, false, F16L>);
   const int items = a.batch * a.nchunks * a.nheads;
   const int grid = persistent_grid(kern, kThreads, items);
   kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(a);
   return hipGetLastError();
 }
 
-template <typename T, typename S>
+template <typename T, typename S, bool F16L = false>
 hipError_t launch_ts(const ChunkStateArgs& a, hipStream_t stream) {
   switch (a.dstate) {
-    case 64: return launch_nk<T, S, 2>(a, stream);
-    case 128: return launch_nk<T, S, 4>(a, stream);
+    case 64: return launch_nk<T, S, 2, F16L>(a, stream);
+    case 128: return launch_nk<T, S, 4, F16L>(a, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -562,6 +593,9 @@ hipError_t launch_chunk_state_persistent(const ChunkStateArgs& a, int dtype, int
   if (state_dtype == SSD_DTYPE_F32) {
     if (dtype == SSD_DTYPE_BF16) return launch_ts<bf16, float>(a, stream);
     if (dtype == SSD_DTYPE_F16) return launch_ts<f16, float>(a, stream);
+  } else if (state_dtype == SSD_STATE_F16S_LOCAL) {
+    if (dtype == SSD_DTYPE_BF16) return launch_ts<bf16, float, true>(a, stream);
+    if (dtype == SSD_DTYPE_F16) return launch_ts<f16, float, true>(a, stream);
   } else if (state_dtype == SSD_DTYPE_BF16) {
     if (dtype == SSD_DTYPE_BF16) return launch_ts<bf16, bf16>(a, stream);
     if (dtype == SSD_DTYPE_F16) return launch_ts<f16, bf16>(a, stream);

@@ -93,6 +93,15 @@ __device__ __forceinline__ void split_weighted(const frag8<T>& b, f32x4 w0, f32x
   }
 }
 
+// SSD_STATE_F16S_LOCAL: the f32 slot, within a [P][N] item, that holds the
+// scale of row p's n tile t (columns 16 t .. 16 t + 15) -- the item's
+// P x N/16 scales, in (p, t) order, packed into the second halves (unused by
+// the f16 values) of its first rows.
+template <int N> __device__ __forceinline__ int f16l_scale_slot(int p, int t) {
+  const int k = p * (N / 16) + t;
+  return (k / (N / 2)) * N + N / 2 + k % (N / 2);
+}
+
 template <typename T> __device__ __forceinline__ frag8<T> zero_frag() {
   frag8<T> z;
 #pragma unroll

@@ -225,7 +225,12 @@ __device__ __forceinline__ float row_max(float m) {
 // threads).  Every load of a row precedes, in the wave's instruction order,
 // the stores into that row, so the in-place writes never overtake a read.
 // The recurrence and final_state stay f32.
-template <int N, int SPT, int UNROLL>
+// F16L: the local states arrive as SSD_STATE_F16S_LOCAL (chunk_state's f16
+// rows, a scale per 16-column tile of each row packed into the second halves
+// of the item's first rows): each thread reads its SPT f16 values (the slots
+// its S_in values then overwrite; SPT divides 16) and their tile's scale,
+// which no store touches; f16 value times a power of two is exact in f32.
+template <int N, int SPT, int UNROLL, bool F16L>
 __global__ __launch_bounds__(256) void state_passing_f16s_kernel(StatePassingArgs p) {
   constexpr int TPR = N / SPT;  // threads per row (SPT = 4 or 8 states per thread)
   typedef typename std::conditional<SPT == 8, f32x8, f32x4>::type V;
@@ -280,7 +285,23 @@ __global__ __launch_bounds__(256) void state_passing_f16s_kernel(StatePassingArg
     *reinterpret_cast<H*>(hrow + c * 2 * cstride) = hv;
     if (col == 0) srow[c * sstride] = __builtin_ldexpf(1.f, e);
   };
-  st = run_chain<UNROLL>(p.nchunks, dec, st, [&](int c, auto nt) { return loadv(elem + c * cstride, nt); }, store_f16s);
+  // F16L: this thread's SPT f16 local values of chunk c times the row's scale
+  static_assert(16 % SPT == 0, "a thread's states lie in one 16-column tile");
+  const float* rscale = base + f16l_scale_slot<N>(row, col / 16);
+  auto loadh = [&](int c, auto nt) __attribute__((always_inline)) {
+    const H* q = reinterpret_cast<const H*>(hrow + c * 2 * cstride);
+    const H hv = decltype(nt)::value ? __builtin_nontemporal_load(q) : *q;
+    const float sc = rscale[c * cstride];
+    V r;
+#pragma unroll
+    for (int k = 0; k < SPT; ++k) r[k] = (float)hv[k] * sc;
+    return r;
+  };
+  if constexpr (F16L) {
+    st = run_chain<UNROLL>(p.nchunks, dec, st, loadh, store_f16s);
+  } else {
+    st = run_chain<UNROLL>(p.nchunks, dec, st, [&](int c, auto nt) { return loadv(elem + c * cstride, nt); }, store_f16s);
+  }
   if (p.final_state) {
     float* fo = p.final_state + (int64_t)bh * PN + SPT * (int64_t)v;
 #pragma unroll
@@ -301,12 +322,19 @@ hipError_t launch_state_passing(const StatePassingArgs& a, int state_dtype, hipS
     // of C4 fit the device in one wave of workgroups (8 states per thread and
     // batches of 8: 196 VGPRs, 0.53 instead of 0.58 of HBM peak at C4)
     constexpr int spt = 4;
-    if (state_dtype != SSD_DTYPE_F32 || a.split_dtype != 0 || !a.sscale || (PN / spt) % 256 != 0)
+    const bool f16l = state_dtype == SSD_STATE_F16S_LOCAL;
+    if ((state_dtype != SSD_DTYPE_F32 && !f16l) || a.split_dtype != 0 || !a.sscale || (PN / spt) % 256 != 0)
       return hipErrorInvalidValue;
     const dim3 grid((unsigned)(chains * ((PN / spt + 255) / 256)));
-    if (a.dstate == 128) state_passing_f16s_kernel<128, spt, 4><<<grid, 256, 0, stream>>>(a);
-    else if (a.dstate == 64) state_passing_f16s_kernel<64, spt, 4><<<grid, 256, 0, stream>>>(a);
-    else return hipErrorInvalidValue;
+    if (a.dstate == 128) {
+      if (f16l) state_passing_f16s_kernel<128, spt, 4, true><<<grid, 256, 0, stream>>>(a);
+      else state_passing_f16s_kernel<128, spt, 4, false><<<grid, 256, 0, stream>>>(a);
+    } else if (a.dstate == 64) {
+      if (f16l) state_passing_f16s_kernel<64, spt, 4, true><<<grid, 256, 0, stream>>>(a);
+      else state_passing_f16s_kernel<64, spt, 4, false><<<grid, 256, 0, stream>>>(a);
+    } else {
+      return hipErrorInvalidValue;
+    }
     return hipGetLastError();
   }
   if (a.split_dtype != 0) {

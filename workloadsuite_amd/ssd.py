@@ -50,6 +50,7 @@ __all__ = [
     "workspace_bytes",
     "SSDError",
     "F16SStates",
+    "F16SLocalStates",
 ]
 
 SSDError = _lib.SSDError
@@ -73,6 +74,27 @@ class F16SStates(NamedTuple):
     def decode(self) -> torch.Tensor:
         N = self.states.shape[-1]
         return self.states.view(torch.float16)[..., :N].float() * self.scales[..., None]
+
+
+class F16SLocalStates(NamedTuple):
+    """Local states as ``chunk_state(..., state_dtype="f16s")`` writes them
+    (SSD_STATE_F16S_LOCAL): ``states`` [b, c, h, P, N] float32 storage whose
+    rows hold N f16 values in their first half; the power-of-two scales of
+    each [P, N] item, one per row p and 16-column tile t, sit in (p, t) order
+    in the second halves of its first rows; state[..., p, n] = f16 value *
+    scale[p, n // 16].  ``state_passing`` takes them in place of f32 local
+    states."""
+    states: torch.Tensor
+
+    def scales(self) -> torch.Tensor:
+        """[b, c, h, P, N / 16] float32: the scale of each row's 16-column tiles."""
+        P, N = self.states.shape[-2:]
+        rows = P * (N // 16) // (N // 2)
+        return self.states[..., :rows, N // 2:].reshape(*self.states.shape[:-2], P, N // 16)
+
+    def decode(self) -> torch.Tensor:
+        N = self.states.shape[-1]
+        return self.states.view(torch.float16)[..., :N].float() * self.scales().repeat_interleave(16, -1)
 
 
 def _handover(state_format, dtype, state_dtype):
@@ -334,7 +356,12 @@ def chunk_prep(B, C, chunk_size):
 
 
 def chunk_state(X, B, Acs, dt=None, state_dtype=torch.float32, prep=None):
-    """K2: local states [b, c, h, P, N] (MR:144, 148-149).  ``prep``: chunk_prep(B, C, Q) or None."""
+    """K2: local states [b, c, h, P, N] (MR:144, 148-149).  ``prep``: chunk_prep(B, C, Q) or None.
+
+    ``state_dtype="f16s"`` (16-bit inputs at chunk 256, d_state 64 / 128):
+    the f32 local states rounded to f16 rows with a power-of-two scale per
+    row, as an ``F16SLocalStates`` (what the forward hands from K2 to K3
+    there when S_in goes to chunk_scan as "f16s")."""
     b, L, h, P = X.shape
     g, N = B.shape[2], B.shape[3]
     Q = Acs.shape[-1]
@@ -343,17 +370,18 @@ def chunk_state(X, B, Acs, dt=None, state_dtype=torch.float32, prep=None):
     _expect("Acs", Acs, (b, h, L // Q, Q))
     _expect("dt", dt, (b, L, h))
     _check_prep(prep, d)
-    if state_dtype not in _STATE_DTYPES:
+    f16l = isinstance(state_dtype, str) and state_dtype == "f16s"
+    if not f16l and state_dtype not in _STATE_DTYPES:
         raise ValueError(f"unsupported state dtype {state_dtype}")
     X, Bm = _vec_operand(X.detach()), _vec_operand(B.detach())
     Acs = _f32_contig(Acs)
     dt = _f32_operand(dt)
-    states = torch.empty((b, L // Q, h, P, N), dtype=state_dtype, device=dev)
+    states = torch.empty((b, L // Q, h, P, N), dtype=torch.float32 if f16l else state_dtype, device=dev)
     _lib.check(_lib.load().ssd_chunk_state(
         ctypes.byref(d), _DTYPES[X.dtype], _ptr(X), _lib.strides(X), _ptr(Bm), _lib.strides(Bm),
         _ptr(dt), _lib.strides(dt) if dt is not None else None, _ptr(Acs), _ptr(states),
-        _STATE_DTYPES[state_dtype], _ptr(prep), _stream(dev)))
-    return states
+        _lib.STATE_F16S_LOCAL if f16l else _STATE_DTYPES[state_dtype], _ptr(prep), _stream(dev)))
+    return F16SLocalStates(states) if f16l else states
 
 
 def state_passing(states, chunk_decay, initial_states=None, return_final_states=True, split=None):
@@ -363,19 +391,28 @@ def state_passing(states, chunk_decay, initial_states=None, return_final_states=
     (f32 states only): torch.bfloat16 / torch.float16 store S_in as that
     type's (hi, lo) pairs for ``chunk_scan(..., split=True)``; "f16s" as f16
     rows with a power-of-two scale per row for ``chunk_scan(..., split="f16s")``.
+    ``states`` may be ``chunk_state(..., state_dtype="f16s")``'s
+    ``F16SLocalStates`` (S_in then goes out as "f16s").
     """
+    local = isinstance(states, F16SLocalStates)
+    if local:
+        if split not in (None, "f16s"):
+            raise ValueError('f16 local states give f16s S_in: split must be "f16s" or None')
+        split, states = "f16s", states.states
     S = states.detach().clone(memory_format=torch.contiguous_format)
     final = (torch.empty((S.shape[0], S.shape[2], S.shape[3], S.shape[4]), dtype=torch.float32, device=S.device)
              if return_final_states else None)
     scales = torch.empty(S.shape[:4], dtype=torch.float32, device=S.device) if split == "f16s" else None
-    state_passing_(S, chunk_decay, initial_states, final, split=split, scales=scales)
+    state_passing_(S, chunk_decay, initial_states, final, split=split, scales=scales, f16_local=local)
     return (F16SStates(S, scales) if scales is not None else S), final
 
 
-def state_passing_(states, chunk_decay, initial_states=None, final_states=None, split=None, scales=None):
+def state_passing_(states, chunk_decay, initial_states=None, final_states=None, split=None, scales=None,
+                   f16_local=False):
     """K3 in place on a contiguous ``states`` buffer (local states in, S_in out);
     ``final_states`` (optional, [b, h, P, N] float32) receives the last state;
-    ``scales`` ([b, c, h, P] float32) the row scales when split="f16s"."""
+    ``scales`` ([b, c, h, P] float32) the row scales when split="f16s";
+    ``f16_local``: the buffer holds SSD_STATE_F16S_LOCAL local states (split "f16s")."""
     b, nc, h, P, N = states.shape
     dev = _device_check(states, chunk_decay, initial_states, final_states)
     if not states.is_contiguous():
@@ -393,6 +430,10 @@ def state_passing_(states, chunk_decay, initial_states=None, final_states=None, 
     if split is not None and (states.dtype != torch.float32 or split not in _SPLIT_STATES):
         raise ValueError('split storage needs float32 states and split=torch.bfloat16, torch.float16 or "f16s"')
     sd = _STATE_DTYPES[states.dtype] if split is None else _SPLIT_STATES[split]
+    if f16_local:
+        if split != "f16s":
+            raise ValueError('f16 local states need split="f16s"')
+        sd = _lib.STATE_F16S_LOCAL
     if split == "f16s":
         _expect("scales", scales, (b, nc, h, P), torch.float32)
         if scales is None or not scales.is_contiguous() or scales.device != dev:
