@@ -12,6 +12,10 @@ points, bit for bit (Y and the final state), with and without dt and an
 initial state, both 16-bit types, both dstates, several groups, for both
 formats in which state_passing hands f32 states to chunk_scan (hi/lo pairs,
 "split"; f16 rows with a power-of-two scale per row, "f16s", the default).
+With "f16s" the local states that cross HBM (chunk_state then
+state_passing; the mixed plan's segments) go as f16 rows, so the per-kernel
+reference passes each chain's local states in the format the forward uses
+for it (tests/state_plans.py).
 The per-kernel path itself is held to the oracle by the parity tests."""
 
 import pytest

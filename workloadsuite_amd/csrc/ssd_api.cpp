@@ -312,7 +312,8 @@ int run_state_passing(const ssd_dims* d, int dtype, const ChunkStateArgs& sa, co
       StatePassingArgs rest = pa;
       rest.bh_begin = plan.nfull;
       rest.bh_count = (int)(chains - plan.nfull);
-      if ((rc = hip_status(ssd::launch_state_passing(rest, state_dtype, s)))) return rc;
+      // (the segments leave f16 local states where S_in goes out as f16s)
+      if ((rc = hip_status(ssd::launch_state_passing(rest, pa.f16s ? SSD_STATE_F16S_LOCAL : state_dtype, s)))) return rc;
     }
     return SSD_OK;
   }

@@ -67,6 +67,26 @@ __device__ __forceinline__ Item item_of(const ChunkStateArgs& p, int it) {
   return r;
 }
 
+// SSD_STATE_F16S_LOCAL store of one lane's 4 local states: row `row`,
+// columns 16 nt + 4 g .. + 3 of the [P][N] item at `item` (f32 layout).  The
+// 16 states of the row in n tile nt are in lanes i, i + 16, i + 32, i + 48
+// (i = row % 16) of the wave: their largest magnitude takes two lane swaps,
+// and sets the tile row's power-of-two scale (largest |v| in [2^14, 2^15]).
+template <int N>
+__device__ __forceinline__ void store_f16l(float* item, int row, int nt, int g, f32x4 v) {
+  float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+  m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
+  f16x4 hv;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) hv[k] = (f16)__builtin_ldexpf(v[k], -e);
+  *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;
+  if (g == 0) item[f16l_scale_slot<N>(row, nt)] = __builtin_ldexpf(1.f, e);
+}
+
 template <typename S> struct StateStore;
 template <> struct StateStore<float> {
   __device__ static void store(float* p, f32x4 v) { *reinterpret_cast<f32x4*>(p) = v; }
@@ -211,22 +231,7 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
   auto store_state = [&](const Item& r, int q) __attribute__((always_inline)) {
     S* sg = reinterpret_cast<S*>(p.states) + (((int64_t)r.b * p.nchunks + r.c) * p.nheads + r.h) * (int64_t)(kP * N);
     if constexpr (F16L) {
-      // the largest |state| of row 16 (pt0 + q) + i in this wave's n tile:
-      // swap with the neighbouring 16-lane row, then with the other 32-lane half
-      const f32x4 v = st_prev[q];
-      float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-      m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-      m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-      const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
-      f16x4 hv;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) hv[k] = (f16)__builtin_ldexpf(v[k], -e);
-      const int row = 16 * (pt0 + q) + i;
-      float* item = reinterpret_cast<float*>(sg);
-      *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;
-      if (g == 0) item[f16l_scale_slot<N>(row, nt)] = __builtin_ldexpf(1.f, e);
+      store_f16l<N>(reinterpret_cast<float*>(sg), 16 * (pt0 + q) + i, nt, g, st_prev[q]);
     } else {
       StateStore<S>::store(sg + srow + 16 * N * q, st_prev[q]);
     }
@@ -338,8 +343,9 @@ hipError_t launch_ts(const ChunkStateArgs& a, hipStream_t stream) {
 // Workgroups [0, plan.nfull) walk the whole chains bh = blockIdx.  Each of
 // the rest takes plan.seg_len chunks of one of the remaining chains (chains
 // nfull, nfull + 1, ...; plan.seg_per_chain segments each) and writes those
-// chunks' f32 local states, exactly as chunk_state would, for state_passing
-// to finish: with 1.25 chains per CU the whole chains take one workgroup slot
+// chunks' local states, exactly as chunk_state would (f32, or with the f16s
+// hand-over its f16 rows, SSD_STATE_F16S_LOCAL), for state_passing to
+// finish: with 1.25 chains per CU the whole chains take one workgroup slot
 // of every CU and the segments the second.
 template <typename T, int NK, bool HAS_DT, bool F16S>
 __global__ __launch_bounds__(64 * kNW) __attribute__((amdgpu_waves_per_eu(4)))
@@ -489,10 +495,13 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
     }
   };
 
-  // a segment's local state of chunk c (f32, chunk_state's layout)
+  // a segment's local state of chunk c in chunk_state's layout: f32, or with
+  // the f16s hand-over as chunk_state's f16 rows (SSD_STATE_F16S_LOCAL) for
+  // state_passing to finish
   auto store_local = [&](int c, int q) __attribute__((always_inline)) {
     float* sg = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (int64_t)(kP * N);
-    *reinterpret_cast<f32x4*>(sg + srow + 16 * N * q) = st[q];
+    if constexpr (F16S) store_f16l<N>(sg, 16 * (pt0 + q) + i, nt, g, st[q]);
+    else *reinterpret_cast<f32x4*>(sg + srow + 16 * N * q) = st[q];
   };
 
   frag8<T> bt[kKS];
