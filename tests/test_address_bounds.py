@@ -14,11 +14,12 @@ strided views) and every LDS byte inside its buffer.
 
 Kernels per shape: C3, C4 and the R0 layer span (16-bit, chunk 256) run
 chunk_prep, the persistent chunk_state / chunk_scan and the state chain; C2
-and C5 (f32, chunk 64 / 128) the f32 chunk_scan, chunk_state and chain; every
-shape runs state_passing.  C1 (d_state 16) and R0's core at chunk 64 run only
-the generic chunk_state / chunk_scan besides, whose staging loops bound every
-row and column by the shape explicitly (ssd_device.h stage_rows /
-stage_transposed) instead of by lane arithmetic.
+and C5 (f32, chunk 64 / 128) the f32 chunk_scan, chunk_state and chain, and
+R0's core (16-bit inputs at chunk 64) the same chunk_state and chain on
+16-bit staged rows; every shape runs state_passing.  C1 (d_state 16) and R0's
+chunk_scan run the generic kernels, whose staging loops bound every row and
+column by the shape explicitly (ssd_device.h stage_rows / stage_transposed)
+instead of by lane arithmetic.
 
 The restatements are pinned to the source: each check first asserts that
 the lines it restates still read as below in the kernel file
@@ -386,7 +387,7 @@ def f32_units(B, L, H, Q, G):
     return h0, h1
 
 
-@pytest.mark.parametrize("name", ["C2", "C5"])
+@pytest.mark.parametrize("name", ["C2", "C5", "R0"])
 def test_f32_kernel_addresses(name):
     B, L, H, P, N, Q, G, _ = SHAPES[name]
     assert P == 64 and Q in (64, 128) and N in (64, 128)
@@ -409,8 +410,12 @@ def test_f32_kernel_addresses(name):
         "const int row = 32 * sb + 16 * st + i, pc = 8 * kc + 2 * g;",
         "bf8.hi = *reinterpret_cast<const f32x4*>(brow + 4 * ((pc + 1) ^ (row & 7)));")
     pin("ssd_chunk_state_f32.hip",
-        "const int ppr = cols / 4, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ (4 * ((r >> 2) & 3));",
-        "dma16_at(src + r * ld + 4 * pc, dst + (uint32_t)(blk * 1024));",
+        "return (sizeof(T) == 4 ? 4 : 2) * ((l >> 2) & 3);",
+        "return l * cols + EPP * ((col / EPP) ^ swz_x<T>(l)) + col % EPP;",
+        "const int ppr = cols * (int)sizeof(T) / 16, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ swz_x<T>(r);",
+        "dma16_at(src + r * ld + (16 / (int)sizeof(T)) * pc, dst + (uint32_t)(blk * 1024));",
+        "constexpr int XPW = Q * kP * ES / 1024 / kNW;",
+        "constexpr int BPW = Q * N * ES / 1024 / kNW;",
         "*reinterpret_cast<f32x4*>(sg + (16 * (2 * pp + a) + i) * N + 16 * (nt0 + n) + 4 * g) = acc[a][n];",
         "return (16 * (2 * pp + a) + i) * N + 16 * (nt0 + n) + 4 * g;",
         "*reinterpret_cast<f32x4*>(sg + sidx(a, n)) = st[a][n];",
@@ -451,16 +456,28 @@ def test_f32_kernel_addresses(name):
     inside("chunk_scan B fragment rows", 32 * sb_ + 16 * st_ + i, 0, Q)
     bpc = 8 * np.arange(N // 32)[:, None, None, None] + 2 * g[..., None] + np.arange(2)
     inside("chunk_scan B fragment floats", 4 * (bpc[..., None] ^ np.arange(8)) + 3, 0, N)
-    # B copies (chunk_state f32, chain): rows of N floats, generic row copy
-    ppr = N // 4
-    bpw = Q * N // 256 // 8
-    bblk = wave + 8 * np.arange(bpw)[:, None, None]
-    br = bblk * (64 // ppr) + lane // ppr
-    inside("B rows", br, 0, Q)
-    inside("B floats", 4 * ((lane % ppr) ^ (4 * ((br >> 2) & 3))) + 3, 0, N)
-    lds_f = max(2 * Q * P, Q * P + Q * N)
-    inside("chunk_state B staging LDS", Q * P * 4 + bblk * 1024 + 16 * lane + 15, 0, lds_f * 4)
-    inside("chain B LDS (2 buffers)", (1 * Q * N) * 4 + bblk * 1024 + 16 * lane + 15, 0, 2 * Q * N * 4)
+    # x and B copies of chunk_state and the chain (stage_rows), for f32 and
+    # 16-bit inputs: rows of `cols` elements in 16-byte pieces, piece k of row
+    # r from piece k ^ swz_x(r); operand reads at swz_off
+    for es in (4, 2):
+        epp = 16 // es
+        swx = lambda r: (4 if es == 4 else 2) * ((r >> 2) & 3)  # noqa: E731
+        lds_e = max(2 * Q * P, Q * P + Q * N)
+        for cols, name in ((P, "x"), (N, "B")):
+            ppr = cols * es // 16
+            ncp = Q * cols * es // 1024
+            assert ncp % 8 == 0, (name, es)
+            cblk = wave + 8 * np.arange(ncp // 8)[:, None, None]
+            cr = cblk * (64 // ppr) + lane // ppr
+            inside(f"{name} rows ({es}-byte)", cr, 0, Q)
+            inside(f"{name} elements ({es}-byte)", epp * ((lane % ppr) ^ swx(cr)) + epp - 1, 0, cols)
+            inside(f"{name} LDS buffer ({es}-byte)", cblk * 1024 + 16 * lane + 15, 0, Q * cols * es)
+            if name == "B":
+                inside("chunk_state B staging LDS", Q * P * es + cblk * 1024 + 16 * lane + 15, 0, lds_e * es)
+            l_ = 32 * np.arange(Q // 32)[:, None, None, None] + 16 * (np.arange(8)[None, :, None, None] >> 2) + 4 * g + (np.arange(8)[None, :, None, None] & 3)
+            col = np.arange(cols)[:, None, None, None, None]
+            off = l_ * cols + epp * ((col // epp) ^ swx(l_)) + col % epp
+            inside(f"{name} operand reads ({es}-byte)", off, 0, Q * cols)
     # Acs and dt copies
     inside("Acs (lanes < Q / 4)", 4 * np.arange(Q // 4) + 3, 0, Q)
     part = np.arange(Q // 64)[:, None]

@@ -170,13 +170,15 @@ F32_SHAPES = [
 ]
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("b,L,h,N,g,Q", F32_SHAPES)
 @pytest.mark.parametrize("with_dt,with_init", [(True, True), (False, False), (False, True)])
-def test_f32_chain_entry_point(b, L, h, N, g, Q, with_dt, with_init):
-    """ssd_chunk_state_passing on f32 inputs and states against chunk_state
-    then state_passing: S_in and the final state bit for bit."""
-    print("CASE f32 chain", b, L, h, N, g, Q, with_dt, with_init, flush=True)
-    X, A, B, C, dt, init = case(torch.float32, b, L, h, 64, N, g, seed=L + h + N)
+def test_f32_chain_entry_point(b, L, h, N, g, Q, with_dt, with_init, dtype):
+    """ssd_chunk_state_passing with f32 states against chunk_state then
+    state_passing: S_in and the final state bit for bit (f32 inputs, and
+    16-bit inputs at chunk 64 / 128, which the same f32-MFMA kernels take)."""
+    print("CASE f32 chain", dtype, b, L, h, N, g, Q, with_dt, with_init, flush=True)
+    X, A, B, C, dt, init = case(dtype, b, L, h, 64, N, g, seed=L + h + N)
     dt = dt if with_dt else None
     init = init if with_init else None
     Acs, decay = S.chunk_cumsum(A, Q)

@@ -300,7 +300,7 @@ int run_state_passing(const ssd_dims* d, int dtype, const ChunkStateArgs& sa, co
   // f32: K2 and K3 as one launch wherever it applies (forward 12% faster at
   // C2's 192 chains of 32 chunks, 7% at C5's 4096 chains of 4)
   if (state_dtype == SSD_DTYPE_F32 && ssd::chunk_state_chain_f32_supported(sa, dtype, pa))
-    return hip_status(ssd::launch_chunk_state_chain_f32(sa, pa, s));
+    return hip_status(ssd::launch_chunk_state_chain_f32(sa, pa, dtype, s));
   ssd::ChainPlan plan = (pa.split_dtype || pa.f16s) ? ssd::chunk_state_chain_plan(sa, dtype) : ssd::ChainPlan{0, 1, 1};
   if (pa.f16s && sa.dstate != 128) plan = ssd::ChainPlan{0, 1, 1};  // the chain's f16s store needs d_state 128
   if (plan.nfull > 0) {

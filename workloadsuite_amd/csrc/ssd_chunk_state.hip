@@ -134,7 +134,7 @@ hipError_t launch_t(const ChunkStateArgs& a, hipStream_t stream) {
 
 hipError_t launch_chunk_state(const ChunkStateArgs& a, int dtype, int state_dtype, hipStream_t stream) {
   if (chunk_state_persistent_supported(a, dtype)) return launch_chunk_state_persistent(a, dtype, state_dtype, stream);
-  if (chunk_state_f32_supported(a, dtype, state_dtype)) return launch_chunk_state_f32(a, stream);
+  if (chunk_state_f32_supported(a, dtype, state_dtype)) return launch_chunk_state_f32(a, dtype, stream);
   if (state_dtype == SSD_DTYPE_F32) {
     if (dtype == SSD_DTYPE_F32) return launch_t<float, float>(a, stream);
     if (dtype == SSD_DTYPE_BF16) return launch_t<bf16, float>(a, stream);

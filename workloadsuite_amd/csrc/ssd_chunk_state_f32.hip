@@ -1,7 +1,10 @@
-// K2 -- chunk_state for f32 inputs and f32 states at chunk 64 / 128 and
-// d_state 64 / 128 (the Mamba-2-130M shape and the grouped short-sequence
-// shape).  Same result as the generic kernel in ssd_chunk_state.hip
-// (workloads/mamba/model_ref.py:144, 148-149):
+// K2 -- chunk_state for f32 states at chunk 64 / 128 and d_state 64 / 128
+// (the Mamba-2-130M shape, the grouped short-sequence shape, and MR's own
+// block_len 64 with 16-bit inputs).  Inputs of type T (f32, bf16 or f16) are
+// staged as they are and converted exactly to f32 as the operands are read,
+// so every product is an f32 MFMA on the inputs' exact values.  Same result
+// as the generic kernel in ssd_chunk_state.hip up to its 16-bit rounding of
+// the weighted operand (workloads/mamba/model_ref.py:144, 148-149):
 //   S[p, n] = sum_l (w[l] x[l, p]) B[l, n],   w[l] = exp(Acs[Q-1] - Acs[l]) dt[l]
 // stored as states[b, c, h, p, n].
 //
@@ -32,10 +35,25 @@ constexpr int kP = 64;
 constexpr int kNW = 8;
 constexpr int kThreads = 64 * kNW;
 
-// float offset of x / B element (l, col) in a staged block of rows of `cols`
-// floats: 16-byte piece col / 4 of row l sits at piece (col / 4) ^ 4 ((l >> 2) & 3)
-__device__ __forceinline__ int swz_off(int l, int col, int cols) {
-  return l * cols + 4 * ((col >> 2) ^ (4 * ((l >> 2) & 3))) + (col & 3);
+// Staged rows of x and B: 16-byte pieces of EPP = 16 / sizeof(T) elements,
+// piece k of row l stored at piece k ^ swz_x(l).  A fragment read takes one
+// column of rows 4 g + jj (g = 0..3): the XOR moves those 4 rows to 4
+// different 64-byte (f32) or 32-byte (16-bit) bank groups.
+template <typename T> __device__ __forceinline__ int swz_x(int l) {
+  return (sizeof(T) == 4 ? 4 : 2) * ((l >> 2) & 3);
+}
+// element offset of x / B element (l, col) in a staged block of rows of `cols` elements
+template <typename T> __device__ __forceinline__ int swz_off(int l, int col, int cols) {
+  constexpr int EPP = 16 / (int)sizeof(T);
+  return l * cols + EPP * ((col / EPP) ^ swz_x<T>(l)) + col % EPP;
+}
+// global -> LDS copy blk (1 KB, 64 lanes x 16 bytes) of rows of `cols`
+// elements of T, rows ld elements apart, into dst + 1 KB blk (piece k of row
+// r from piece k ^ swz_x(r) of the global row)
+template <typename T>
+__device__ __forceinline__ void stage_rows(const T* src, int64_t ld, int cols, int blk, uint32_t dst, int lane) {
+  const int ppr = cols * (int)sizeof(T) / 16, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ swz_x<T>(r);
+  dma16_at(src + r * ld + (16 / (int)sizeof(T)) * pc, dst + (uint32_t)(blk * 1024));
 }
 
 // w[l] = exp(Acs[Q-1] - Acs[l]) dt[l] from Acs[l], log2(e) Acs[Q-1] and dt[l]
@@ -45,17 +63,18 @@ __device__ __forceinline__ float chunk_weight(float acs_l, float last_log2, floa
   return __builtin_amdgcn_exp2f(__builtin_fmaf(acs_l, -kLog2e, last_log2)) * dt_l;
 }
 
-template <int NK, int RT, bool HAS_DT>
+template <typename T, int NK, int RT, bool HAS_DT>
 __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArgs p, int hs, int slices) {
   constexpr int Q = 64 * RT;
   constexpr int N = 32 * NK;
+  constexpr int ES = (int)sizeof(T);
   constexpr int KS = Q / 32;             // K steps of 32 tokens
   constexpr int NTW = N / 64;            // n tiles per wave
-  constexpr int XPW = Q * kP / 256 / kNW;  // x copies (1 KB) per wave and head
-  constexpr int BPW = Q * N / 256 / kNW;   // B copies per wave
+  constexpr int XPW = Q * kP * ES / 1024 / kNW;  // x copies (1 KB) per wave and head
+  constexpr int BPW = Q * N * ES / 1024 / kNW;   // B copies per wave
   // x buffers 0 and 1, then room for B (staged once, over buffer 1)
-  constexpr int LDS_F = 2 * Q * kP > Q * kP + Q * N ? 2 * Q * kP : Q * kP + Q * N;
-  __shared__ __attribute__((aligned(1024))) float lds[LDS_F];
+  constexpr int LDS_E = 2 * Q * kP > Q * kP + Q * N ? 2 * Q * kP : Q * kP + Q * N;
+  __shared__ __attribute__((aligned(1024))) T lds[LDS_E];
   __shared__ __attribute__((aligned(16))) float al[2][Q];
   __shared__ __attribute__((aligned(16))) float dl[HAS_DT ? 2 : 1][HAS_DT ? Q : 4];
 
@@ -74,20 +93,15 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
   if (h0 >= h1) return;  // the whole workgroup, before any barrier
   const int64_t l0 = (int64_t)c * Q;
 
-  const float* xg0 = reinterpret_cast<const float*>(p.x) + b * p.sxb + l0 * p.sxl;
-  const float* bg = reinterpret_cast<const float*>(p.bm) + b * p.sbb + l0 * p.sbl + grp * p.sbg;
+  const T* xg0 = reinterpret_cast<const T*>(p.x) + b * p.sxb + l0 * p.sxl;
+  const T* bg = reinterpret_cast<const T*>(p.bm) + b * p.sbb + l0 * p.sbl + grp * p.sbg;
   const uint32_t lds_base = lds_offset(&lds[0]);
   const uint32_t al_lds = lds_offset(&al[0][0]), dl_lds = lds_offset(&dl[0][0]);
 
-  // rows of `cols` floats, 1 KB copies: copy blk moves rows blk * 1024 / (4 cols) ...
-  auto issue_rows = [&](const float* src, int64_t ld, int cols, int blk, uint32_t dst) __attribute__((always_inline)) {
-    const int ppr = cols / 4, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ (4 * ((r >> 2) & 3));
-    dma16_at(src + r * ld + 4 * pc, dst + (uint32_t)(blk * 1024));
-  };
   auto issue_head = [&](int h, int bf) __attribute__((always_inline)) {
-    const float* xg = xg0 + h * p.sxh;
+    const T* xg = xg0 + h * p.sxh;
 #pragma unroll
-    for (int m = 0; m < XPW; ++m) issue_rows(xg, p.sxl, kP, wave + kNW * m, lds_base + (uint32_t)(bf * Q * kP * 4));
+    for (int m = 0; m < XPW; ++m) stage_rows<T>(xg, p.sxl, kP, wave + kNW * m, lds_base + (uint32_t)(bf * Q * kP * ES), lane);
     if (wave == kNW - 1 && lane < Q / 4) {
       const float* ag = p.acs + (((int64_t)b * p.nheads + h) * p.nchunks + c) * Q;
       dma16_at(ag + 4 * lane, al_lds + (uint32_t)(bf * Q * 4));
@@ -104,19 +118,19 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
   // ---- per slice: B operands of this wave's n tiles, via LDS ----
   issue_head(h0, 0);
 #pragma unroll
-  for (int m = 0; m < BPW; ++m) issue_rows(bg, p.sbl, N, wave + kNW * m, lds_base + (uint32_t)(Q * kP * 4));
+  for (int m = 0; m < BPW; ++m) stage_rows<T>(bg, p.sbl, N, wave + kNW * m, lds_base + (uint32_t)(Q * kP * ES), lane);
   dma_wait();
   __syncthreads();
   frag8<float> bfr[NTW][KS];
   {
-    const float* bl = lds + Q * kP;
+    const T* bl = lds + Q * kP;
 #pragma unroll
     for (int n = 0; n < NTW; ++n)
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          bfr[n][ks][j] = bl[swz_off(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)];
+          bfr[n][ks][j] = to_f32<T>(bl[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)]);
   }
   __syncthreads();  // B's LDS is x buffer 1 from here on
 
@@ -141,7 +155,7 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
     if (hprev >= 0) store_states(hprev);
     if (h + 1 < h1) issue_head(h + 1, bf ^ 1);
     hprev = h;
-    const float* xb = lds + bf * Q * kP;
+    const T* xb = lds + bf * Q * kP;
     const float* ab = al[bf];
     const float last = ab[Q - 1] * kLog2e;
 #pragma unroll
@@ -166,7 +180,7 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
         const int col = 16 * (2 * pp + a) + i;
         frag8<float> xf;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xf[j] = xb[swz_off(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)] * w[j];
+        for (int j = 0; j < 8; ++j) xf[j] = to_f32<T>(xb[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)]) * w[j];
 #pragma unroll
         for (int n = 0; n < NTW; ++n) acc[a][n] = mma(bfr[n][ks], xf, acc[a][n]);
       }
@@ -189,17 +203,18 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
 // states never reach memory.  x and B of the next chunk are copied
 // global -> LDS while the current chunk computes; the chains of one group's
 // heads run on one XCD and share B through its L2.
-template <int NK, int RT, bool HAS_DT, bool DB>
+template <typename T, int NK, int RT, bool HAS_DT, bool DB>
 __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkStateArgs p, StatePassingArgs sp) {
   constexpr int Q = 64 * RT;
   constexpr int N = 32 * NK;
+  constexpr int ES = (int)sizeof(T);
   constexpr int KS = Q / 32;
   constexpr int NTW = N / 64;
-  constexpr int XPW = Q * kP / 256 / kNW;
-  constexpr int BPW = Q * N / 256 / kNW;
+  constexpr int XPW = Q * kP * ES / 1024 / kNW;
+  constexpr int BPW = Q * N * ES / 1024 / kNW;
   constexpr int NBUF = DB ? 2 : 1;
-  __shared__ __attribute__((aligned(1024))) float xs[NBUF][Q * kP];
-  __shared__ __attribute__((aligned(1024))) float bs[NBUF][Q * N];
+  __shared__ __attribute__((aligned(1024))) T xs[NBUF][Q * kP];
+  __shared__ __attribute__((aligned(1024))) T bs[NBUF][Q * N];
   __shared__ __attribute__((aligned(16))) float al[NBUF][Q];
   __shared__ __attribute__((aligned(16))) float dl[HAS_DT ? NBUF : 1][HAS_DT ? Q : 4];
 
@@ -212,21 +227,17 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
   const int h = bh % p.nheads, b = bh / p.nheads;
   const int grp = h / (p.nheads / p.ngroups);
 
-  const float* xg = reinterpret_cast<const float*>(p.x) + b * p.sxb + h * p.sxh;
-  const float* bg = reinterpret_cast<const float*>(p.bm) + b * p.sbb + grp * p.sbg;
+  const T* xg = reinterpret_cast<const T*>(p.x) + b * p.sxb + h * p.sxh;
+  const T* bg = reinterpret_cast<const T*>(p.bm) + b * p.sbb + grp * p.sbg;
   const float* dg = HAS_DT ? p.dt + b * p.sdb + h * p.sdh : nullptr;
   const uint32_t xs_lds = lds_offset(&xs[0][0]), bs_lds = lds_offset(&bs[0][0]);
   const uint32_t al_lds = lds_offset(&al[0][0]), dl_lds = lds_offset(&dl[0][0]);
-  auto issue_rows = [&](const float* src, int64_t ld, int cols, int blk, uint32_t dst) __attribute__((always_inline)) {
-    const int ppr = cols / 4, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ (4 * ((r >> 2) & 3));
-    dma16_at(src + r * ld + 4 * pc, dst + (uint32_t)(blk * 1024));
-  };
   auto issue_chunk = [&](int c, int bf) __attribute__((always_inline)) {
     const int64_t l0 = (int64_t)c * Q;
 #pragma unroll
-    for (int m = 0; m < XPW; ++m) issue_rows(xg + l0 * p.sxl, p.sxl, kP, wave + kNW * m, xs_lds + (uint32_t)(bf * Q * kP * 4));
+    for (int m = 0; m < XPW; ++m) stage_rows<T>(xg + l0 * p.sxl, p.sxl, kP, wave + kNW * m, xs_lds + (uint32_t)(bf * Q * kP * ES), lane);
 #pragma unroll
-    for (int m = 0; m < BPW; ++m) issue_rows(bg + l0 * p.sbl, p.sbl, N, wave + kNW * m, bs_lds + (uint32_t)(bf * Q * N * 4));
+    for (int m = 0; m < BPW; ++m) stage_rows<T>(bg + l0 * p.sbl, p.sbl, N, wave + kNW * m, bs_lds + (uint32_t)(bf * Q * N * ES), lane);
     if (wave == kNW - 1 && lane < Q / 4) {
       const float* ag = p.acs + ((int64_t)bh * p.nchunks + c) * Q;
       dma16_at(ag + 4 * lane, al_lds + (uint32_t)(bf * Q * 4));
@@ -284,8 +295,8 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
       vm_wait<kStores>();
       __syncthreads();
     }
-    const float* xb = xs[bf];
-    const float* bl = bs[bf];
+    const T* xb = xs[bf];
+    const T* bl = bs[bf];
     const float* ab = al[bf];
     const float last = ab[Q - 1] * kLog2e;
     f32x4 acc[2][NTW];
@@ -310,13 +321,13 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
       for (int n = 0; n < NTW; ++n)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          bfr[n][j] = bl[swz_off(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)];
+          bfr[n][j] = to_f32<T>(bl[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)]);
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int col = 16 * (2 * pp + a) + i;
         frag8<float> xf;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xf[j] = xb[swz_off(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)] * w[j];
+        for (int j = 0; j < 8; ++j) xf[j] = to_f32<T>(xb[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)]) * w[j];
 #pragma unroll
         for (int n = 0; n < NTW; ++n) acc[a][n] = mma(bfr[n], xf, acc[a][n]);
       }
@@ -339,7 +350,7 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
   }
 }
 
-template <int NK, int RT>
+template <typename T, int NK, int RT>
 hipError_t launch_chain_qn(const ChunkStateArgs& a, const StatePassingArgs& sp, hipStream_t stream) {
   const int64_t chains = (int64_t)a.batch * a.nheads;
   if (chains > INT32_MAX) return hipErrorInvalidValue;
@@ -349,13 +360,13 @@ hipError_t launch_chain_qn(const ChunkStateArgs& a, const StatePassingArgs& sp, 
   // faster double-buffered, C5 (4096 chains of 4) 3% faster single-buffered
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const bool db = chains < 2 * (int64_t)cus;
-  auto kern = db ? (a.dt ? chunk_state_chain_f32_kernel<NK, RT, true, true> : chunk_state_chain_f32_kernel<NK, RT, false, true>)
-                 : (a.dt ? chunk_state_chain_f32_kernel<NK, RT, true, false> : chunk_state_chain_f32_kernel<NK, RT, false, false>);
+  auto kern = db ? (a.dt ? chunk_state_chain_f32_kernel<T, NK, RT, true, true> : chunk_state_chain_f32_kernel<T, NK, RT, false, true>)
+                 : (a.dt ? chunk_state_chain_f32_kernel<T, NK, RT, true, false> : chunk_state_chain_f32_kernel<T, NK, RT, false, false>);
   kern<<<dim3((unsigned)chains), dim3(kThreads), 0, stream>>>(a, sp);
   return hipGetLastError();
 }
 
-template <int NK, int RT>
+template <typename T, int NK, int RT>
 hipError_t launch_qn(const ChunkStateArgs& a, hipStream_t stream) {
   const int hpg = a.nheads / a.ngroups;
   const int64_t bcg = (int64_t)a.batch * a.nchunks * a.ngroups;
@@ -369,16 +380,29 @@ hipError_t launch_qn(const ChunkStateArgs& a, hipStream_t stream) {
   slices = (hpg + hs - 1) / hs;
   const int64_t grid = bcg * slices;
   if (grid > INT32_MAX) return hipErrorInvalidValue;
-  auto kern = a.dt ? chunk_state_f32_kernel<NK, RT, true> : chunk_state_f32_kernel<NK, RT, false>;
+  auto kern = a.dt ? chunk_state_f32_kernel<T, NK, RT, true> : chunk_state_f32_kernel<T, NK, RT, false>;
   kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(a, hs, slices);
   return hipGetLastError();
+}
+
+template <typename T>
+hipError_t launch_chain_t(const ChunkStateArgs& a, const StatePassingArgs& sp, hipStream_t stream) {
+  if (a.chunk == 64) return a.dstate == 64 ? launch_chain_qn<T, 2, 1>(a, sp, stream) : launch_chain_qn<T, 4, 1>(a, sp, stream);
+  if (a.chunk == 128 && a.dstate == 64) return launch_chain_qn<T, 2, 2>(a, sp, stream);
+  return hipErrorInvalidValue;
+}
+
+template <typename T>
+hipError_t launch_t(const ChunkStateArgs& a, hipStream_t stream) {
+  if (a.chunk == 64) return a.dstate == 64 ? launch_qn<T, 2, 1>(a, stream) : launch_qn<T, 4, 1>(a, stream);
+  return a.dstate == 64 ? launch_qn<T, 2, 2>(a, stream) : launch_qn<T, 4, 2>(a, stream);
 }
 
 }  // namespace
 
 bool chunk_state_f32_supported(const ChunkStateArgs& a, int dtype, int state_dtype) {
-  return dtype == SSD_DTYPE_F32 && state_dtype == SSD_DTYPE_F32 && (a.chunk == 64 || a.chunk == 128) &&
-         (a.dstate == 64 || a.dstate == 128);
+  return (dtype == SSD_DTYPE_F32 || dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16) &&
+         state_dtype == SSD_DTYPE_F32 && (a.chunk == 64 || a.chunk == 128) && (a.dstate == 64 || a.dstate == 128);
 }
 
 bool chunk_state_chain_f32_supported(const ChunkStateArgs& a, int dtype, const StatePassingArgs& sp) {
@@ -387,15 +411,16 @@ bool chunk_state_chain_f32_supported(const ChunkStateArgs& a, int dtype, const S
          !sp.f16s && sp.bh_begin == 0 && (sp.bh_count == 0 || sp.bh_count == a.batch * a.nheads);
 }
 
-hipError_t launch_chunk_state_chain_f32(const ChunkStateArgs& a, const StatePassingArgs& sp, hipStream_t stream) {
-  if (a.chunk == 64) return a.dstate == 64 ? launch_chain_qn<2, 1>(a, sp, stream) : launch_chain_qn<4, 1>(a, sp, stream);
-  if (a.chunk == 128 && a.dstate == 64) return launch_chain_qn<2, 2>(a, sp, stream);
-  return hipErrorInvalidValue;
+hipError_t launch_chunk_state_chain_f32(const ChunkStateArgs& a, const StatePassingArgs& sp, int dtype, hipStream_t stream) {
+  if (dtype == SSD_DTYPE_BF16) return launch_chain_t<bf16>(a, sp, stream);
+  if (dtype == SSD_DTYPE_F16) return launch_chain_t<f16>(a, sp, stream);
+  return launch_chain_t<float>(a, sp, stream);
 }
 
-hipError_t launch_chunk_state_f32(const ChunkStateArgs& a, hipStream_t stream) {
-  if (a.chunk == 64) return a.dstate == 64 ? launch_qn<2, 1>(a, stream) : launch_qn<4, 1>(a, stream);
-  return a.dstate == 64 ? launch_qn<2, 2>(a, stream) : launch_qn<4, 2>(a, stream);
+hipError_t launch_chunk_state_f32(const ChunkStateArgs& a, int dtype, hipStream_t stream) {
+  if (dtype == SSD_DTYPE_BF16) return launch_t<bf16>(a, stream);
+  if (dtype == SSD_DTYPE_F16) return launch_t<f16>(a, stream);
+  return launch_t<float>(a, stream);
 }
 
 }  // namespace ssd
