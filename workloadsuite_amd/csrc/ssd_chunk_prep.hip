@@ -53,7 +53,8 @@ __device__ __forceinline__ void prep_body(const ChunkPrepArgs& p, int bcg, unsig
   constexpr int NTILE = N / 16;
   unsigned char* bl = lds;
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int g = lane >> 4, i = lane & 15;
   const int grp = bcg % p.ngroups, bc = bcg / p.ngroups;
   const int c = bc % p.nchunks, b = bc / p.nchunks;

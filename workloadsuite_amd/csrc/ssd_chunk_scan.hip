@@ -64,7 +64,8 @@ __global__ __launch_bounds__(256, (scan_blocks_per_cu<T, NK, RT>())) void chunk_
   __shared__ __attribute__((aligned(16))) T xt_lds[kP * LDS_X];
   __shared__ float dt_l[Q];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, i = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int N = p.dstate;
   const int nblocks = p.batch * p.nchunks * p.nheads;
   const int blk = xcd_remap(blockIdx.x, nblocks);

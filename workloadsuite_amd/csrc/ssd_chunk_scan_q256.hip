@@ -156,7 +156,8 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   // F16S: the per-row scales of S_in, current and next item
   __shared__ __attribute__((aligned(16))) float scl[2][F16S ? kP : 4];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   __builtin_assume(wave < kNW);  // lets the tile-range tests below fold
   const int g = lane >> 4, i = lane & 15;
   const int nitems = p.batch * p.nchunks * p.nheads;
@@ -311,11 +312,21 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
   auto c_to_f16 = [&]() __attribute__((always_inline)) {
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
+      // largest |value| from the bf16 bit patterns (sign cleared, the order
+      // of non-negative bf16 values is that of their bits): no f32
+      // temporaries live across the row's 8 NK values (called for bf16 only)
       float m = 0.f;
+      if constexpr (std::is_same<T, bf16>::value) {
+        typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+        uint32_t mb = 0;
 #pragma unroll
-      for (int kc = 0; kc < NK; ++kc)
+        for (int kc = 0; kc < NK; ++kc) {
+          const auto w = __builtin_bit_cast(u32x4, cf[t][kc]);
 #pragma unroll
-        for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(to_f32<T>(cf[t][kc][j])));
+          for (int j = 0; j < 4; ++j) mb = max(mb, max(w[j] & 0x7fffu, (w[j] >> 16) & 0x7fffu));
+        }
+        m = __uint_as_float(min(mb, 0x7f80u) << 16);  // a NaN counts as inf, as in every lane
+      }
       // the row's 4 lane groups (lanes i, i + 16, i + 32, i + 48)
       m = fmaxf(m, __shfl_xor(m, 16));
       m = fmaxf(m, __shfl_xor(m, 32));
@@ -377,19 +388,19 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
       // (reverse order, so step j of either tile sits at a compile-time index)
       const bool first = k < KA;
       const int t = first ? ta : tb, sb = first ? k : kNPair - 1 - k;
-      frag8<T> bfr[2][NK], cfx[NK];
+      frag8<T> cfx[NK];
 #pragma unroll
-      for (int kc = 0; kc < NK; ++kc) {
-        cfx[kc] = first ? cf[0][kc] : cf[1][kc];
-#pragma unroll
-        for (int st = 0; st < 2; ++st)
-          bfr[st][kc] = load8<T>(bg + (int64_t)(32 * sb + 16 * st + i) * p.sbl + 32 * kc + 8 * g);
-      }
+      for (int kc = 0; kc < NK; ++kc) cfx[kc] = first ? cf[0][kc] : cf[1][kc];
 #pragma unroll
       for (int st = 0; st < 2; ++st) {
+        // one 16-row sub-tile of B at a time (fewer registers live beside
+        // the CB^T blocks; this path runs once per group)
+        frag8<T> bfr[NK];
+#pragma unroll
+        for (int kc = 0; kc < NK; ++kc) bfr[kc] = load8<T>(bg + (int64_t)(32 * sb + 16 * st + i) * p.sbl + 32 * kc + 8 * g);
         f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int kc = 0; kc < NK; ++kc) d = mma(bfr[st][kc], cfx[kc], d);
+        for (int kc = 0; kc < NK; ++kc) d = mma(bfr[kc], cfx[kc], d);
         const bool live = 2 * sb + st <= t;
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) d[jj] = live ? d[jj] : 0.f;

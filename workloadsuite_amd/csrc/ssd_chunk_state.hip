@@ -43,7 +43,8 @@ __global__ __launch_bounds__(256) void chunk_state_kernel(ChunkStateArgs p) {
   __shared__ __attribute__((aligned(16))) T xt_lo[SPLIT ? kP * LDP : 8];
   __shared__ __attribute__((aligned(16))) T bt[N * LDP];
 
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, i = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, i = lane & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int nblocks = p.batch * p.nchunks * p.nheads;
   const int blk = xcd_remap(blockIdx.x, nblocks);
   const int h = blk % p.nheads;

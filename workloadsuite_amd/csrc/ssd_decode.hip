@@ -26,7 +26,8 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs p) {
   constexpr int LPR = N / 4;        // lanes per state row
   constexpr int RPI = 64 / LPR;     // rows per wave instruction
   constexpr int ITERS = 16 / RPI;   // instructions per wave (16 rows)
-  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform: scalar registers
   const int bh = blockIdx.x;
   const int h = bh % p.nheads, b = bh / p.nheads;
   const int grp = h / (p.nheads / p.ngroups);

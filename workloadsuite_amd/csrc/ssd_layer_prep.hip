@@ -62,7 +62,8 @@ __device__ __forceinline__ float silu(float v) {
 // grid: (channel vectors / 64 rounded up) x (runs / kWavesPerBlock rounded up) x batch
 template <typename T, int V, int K>
 __global__ __launch_bounds__(64 * kWavesPerBlock) void conv_silu_kernel(ConvArgs p) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar registers
   const int nvec = p.channels / V;
   const int cv = blockIdx.x * 64 + lane;
   const int run = blockIdx.y * kWavesPerBlock + wave;
