@@ -88,6 +88,7 @@ struct ScanArgs32 {
 
 struct Item {
   int b, c, h, grp;
+  int hg;  // head within the group
 };
 
 // State storage tag: f32 states handed over as f16 with a power-of-two scale
@@ -120,7 +121,27 @@ __device__ __forceinline__ Item item_of(const ScanArgs32& p, int it) {
   const int bc = it / p.nheads;
   r.c = bc % p.nchunks;
   r.b = bc / p.nchunks;
-  r.grp = r.h / (p.nheads / p.ngroups);
+  const int hpg = p.nheads / p.ngroups;
+  r.grp = r.h / hpg;
+  r.hg = r.h - r.grp * hpg;
+  return r;
+}
+
+// The item after r in (b, c, h) order, heads fastest: item_of(it + 1)
+// without its integer divisions (hpg = heads per group).
+__device__ __forceinline__ Item next_item(const ScanArgs32& p, Item r, int hpg) {
+  ++r.h;
+  if (++r.hg == hpg) {
+    r.hg = 0;
+    ++r.grp;
+  }
+  if (r.h == p.nheads) {
+    r.h = r.grp = r.hg = 0;
+    if (++r.c == p.nchunks) {
+      r.c = 0;
+      ++r.b;
+    }
+  }
   return r;
 }
 
@@ -442,7 +463,6 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     // off-diagonal: acc[s2][pt] = S_in[p, :] . C[l, :], then * exp(Acs[l])
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) {
-      set_prio(3);  // waves behind in the item go first
       off_step(pt);
 #pragma unroll
       for (int kc = 0; kc < NK; ++kc) {
@@ -549,7 +569,6 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     // diagonal, step j: s block j of tile ta (j < KA) and of tile tb (j < KB)
 #pragma unroll
     for (int j = 0; j < kNPair - 1; ++j) {
-      set_prio(2 - (j + 1) / 3);
       const bool do_a = j < KA, do_b = j < KB;  // wave-uniform
       if (!do_b) continue;                       // KB >= KA: nothing left for either tile
       f32x4 gs[2];
@@ -669,10 +688,11 @@ void chunk_scan_q256_kernel(ScanArgs32 p) {
     convert(0);
     __syncthreads();
   }
+  const int hpg = p.nheads / p.ngroups;
   for (int it = it0; it < it1; ++it) {
     const int bc = (it - it0) & 1, bn = bc ^ 1;
     const bool has_next = it + 1 < it1;
-    const Item nxt = has_next ? item_of(p, it + 1) : cur;
+    const Item nxt = has_next ? next_item(p, cur, hpg) : cur;
     compute(bc, cur, [&](int pt) __attribute__((always_inline)) {
       if (has_next) issue_copy_part(nxt, bn, pt);
     });

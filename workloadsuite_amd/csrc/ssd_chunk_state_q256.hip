@@ -55,6 +55,7 @@ constexpr int kXBlocks = kQ / 8;     // 1 KB copy blocks of x (8 rows of 64 x 16
 
 struct Item {
   int b, c, h, grp;
+  int hg;  // head within the group
 };
 
 __device__ __forceinline__ Item item_of(const ChunkStateArgs& p, int it) {
@@ -63,7 +64,27 @@ __device__ __forceinline__ Item item_of(const ChunkStateArgs& p, int it) {
   const int bc = it / p.nheads;
   r.c = bc % p.nchunks;
   r.b = bc / p.nchunks;
-  r.grp = r.h / (p.nheads / p.ngroups);
+  const int hpg = p.nheads / p.ngroups;
+  r.grp = r.h / hpg;
+  r.hg = r.h - r.grp * hpg;
+  return r;
+}
+
+// The item after r in (b, c, h) order, heads fastest: item_of(it + 1)
+// without its integer divisions (hpg = heads per group).
+__device__ __forceinline__ Item next_item(const ChunkStateArgs& p, Item r, int hpg) {
+  ++r.h;
+  if (++r.hg == hpg) {
+    r.hg = 0;
+    ++r.grp;
+  }
+  if (r.h == p.nheads) {
+    r.h = r.grp = r.hg = 0;
+    if (++r.c == p.nchunks) {
+      r.c = 0;
+      ++r.b;
+    }
+  }
   return r;
 }
 
@@ -244,6 +265,7 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
   // between its K steps; then wait for the copy, publish it, tabulate its
   // weights, and publish those.
   const int nsteps = (it1 - it0 + 1) / 2;
+  const int hpg = p.nheads / p.ngroups;
   Item cur = item_of(p, it0 + half), prev = cur;
   const bool any = it0 + half < it1;
   if (any) {
@@ -259,7 +281,7 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
     const int it = it0 + half + 2 * k;
     const int bc = k & 1, bn = bc ^ 1;
     const bool active = it < it1, has_next = it + 2 < it1;
-    const Item nxt = has_next ? item_of(p, it + 2) : cur;
+    const Item nxt = has_next ? next_item(p, next_item(p, cur, hpg), hpg) : cur;
     const bool has_prev = k > 0;
     if (active) {
       // copy parts in steps 0..3, the previous item's state stores after them
