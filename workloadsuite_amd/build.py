@@ -30,6 +30,7 @@ SOURCES = [
     "ssd_chunk_state_f32.hip",
     "ssd_state_passing.hip",
     "ssd_chunk_scan.hip",
+    "ssd_chunk_scan_b16.hip",
     "ssd_chunk_scan_q256.hip",
     "ssd_chunk_scan_f32.hip",
     "ssd_layer_prep.hip",

@@ -205,5 +205,11 @@ hipError_t launch_chunk_state_f32(const ChunkStateArgs& a, int dtype, hipStream_
 bool chunk_state_chain_f32_supported(const ChunkStateArgs& a, int dtype, const StatePassingArgs& sp);
 hipError_t launch_chunk_state_chain_f32(const ChunkStateArgs& a, const StatePassingArgs& sp, int dtype, hipStream_t stream);
 hipError_t launch_chunk_scan_f32(const ChunkScanArgs& a, hipStream_t stream);
+// chunk_scan for 16-bit inputs with f32 states at chunk 64 / 128, d_state
+// 64 / 128, without the layer epilogue (ssd_chunk_scan_b16.hip): the f32
+// kernel's decomposition on 16-bit MFMAs; launch_chunk_scan dispatches to it
+// when supported.
+bool chunk_scan_b16_supported(const ChunkScanArgs& a, int dtype, int state_dtype);
+hipError_t launch_chunk_scan_b16(const ChunkScanArgs& a, int dtype, hipStream_t stream);
 
 }  // namespace ssd
