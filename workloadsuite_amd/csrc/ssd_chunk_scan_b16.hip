@@ -10,9 +10,12 @@
 // group before MR:143 contracts them), so one workgroup of 8 waves takes one
 // (b, c, group) -- or a slice of its heads when there are few groups -- forms
 // the causal C.B^T sub-tiles of its rows once, in registers, and walks the
-// heads with x, S_in, Acs and dt copied global -> LDS one head ahead.  Wave w
-// owns row tiles t (chunk 64: t = w % 4 for w < 4, 3 - w % 4 above; chunk
-// 128: w % 4 and 7 - w % 4) and p tiles 2 (w / 4), 2 (w / 4) + 1.
+// heads with x, Acs and dt copied global -> LDS one head ahead (two buffers)
+// and S_in into one buffer, copied under the diagonal part of the previous
+// head once its off-diagonal part has read it: 49 KB of LDS at d_state 128,
+// two workgroups per CU (double-buffered S_in, 81 KB and one per CU, was 12%
+// slower).  Wave w owns row tiles t (chunk 64: t = w % 4 for w < 4, 3 - w % 4
+// above; chunk 128: w % 4 and 7 - w % 4) and p tiles 2 (w / 4), 2 (w / 4) + 1.
 //
 // The products run on 16x16x32 MFMAs of the input type, as in the chunk-256
 // kernel (ssd_chunk_scan_q256.hip):
@@ -50,7 +53,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
   constexpr int NSB = 2 * RT;                // 32-token s blocks of the chunk
   static_assert(XPW >= 1 && SPW >= 1 && BPW >= 1, "copies per wave");
   __shared__ __attribute__((aligned(1024))) T xs[2][Q * kP];
-  __shared__ __attribute__((aligned(1024))) float ss[2][kP * N];
+  __shared__ __attribute__((aligned(1024))) float ss[kP * N];
   __shared__ __attribute__((aligned(16))) float al[2][Q];
   __shared__ __attribute__((aligned(16))) float dl[HAS_DT ? 2 : 1][HAS_DT ? Q : 4];
 
@@ -78,11 +81,11 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
   const T* cg = reinterpret_cast<const T*>(p.cm) + b * p.scb + l0 * p.scl + grp * p.scg;
   T* yg0 = reinterpret_cast<T*>(p.y) + b * p.syb + l0 * p.syl;
 
-  // ---- per-head copies into buffer bf ----
+  // ---- per-head copies: x, Acs, dt into buffer bf, S_in into its buffer ----
   // x rows s (64 elements, 8 pieces): copy block blk holds rows 8 blk ..
   // 8 blk + 7, piece k of row s at slot k ^ (s & 7).  S_in rows r (N floats):
   // piece k at slot k ^ (r & 7).
-  const uint32_t xs_lds = lds_offset(&xs[0][0]), ss_lds = lds_offset(&ss[0][0]);
+  const uint32_t xs_lds = lds_offset(&xs[0][0]), ss_lds = lds_offset(&ss[0]);
   const uint32_t al_lds = lds_offset(&al[0][0]), dl_lds = lds_offset(&dl[0][0]);
   const int64_t xcopy = (int64_t)(lane >> 3) * p.sxl + 8 * ((lane & 7) ^ (lane >> 3));
   auto issue_head = [&](int h, int bf) __attribute__((always_inline)) {
@@ -91,12 +94,6 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
     for (int m = 0; m < XPW; ++m) {
       const int blk = wave + kNW * m;
       dma16_at(xg + (int64_t)(8 * blk) * p.sxl, xs_lds + (uint32_t)((bf * Q * kP) * 2 + blk * 1024));
-    }
-    const float* sg = reinterpret_cast<const float*>(p.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (kP * N);
-#pragma unroll
-    for (int m = 0; m < SPW; ++m) {
-      const int blk = wave + kNW * m, r = blk * (64 / SPR) + lane / SPR, pc = (lane % SPR) ^ (r & 7);
-      dma16_at(sg + r * N + 4 * pc, ss_lds + (uint32_t)((bf * kP * N + blk * 256) * 4));
     }
     if (wave == kNW - 1 && lane < Q / 4) {
       const float* ag = p.acs + (((int64_t)b * p.nheads + h) * p.nchunks + c) * Q;
@@ -110,14 +107,23 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
       }
     }
   };
-  // f32 S_in of buffer bf -> MFMA operand pairs in place: each 32-byte pair
+  // S_in of head h into its (single) buffer
+  auto issue_sin = [&](int h) __attribute__((always_inline)) {
+    const float* sg = reinterpret_cast<const float*>(p.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (kP * N);
+#pragma unroll
+    for (int m = 0; m < SPW; ++m) {
+      const int blk = wave + kNW * m, r = blk * (64 / SPR) + lane / SPR, pc = (lane % SPR) ^ (r & 7);
+      dma16_at(sg + r * N + 4 * pc, ss_lds + (uint32_t)(blk * 1024));
+    }
+  };
+  // f32 S_in -> MFMA operand pairs in place: each 32-byte pair
   // of pieces (8 states) becomes [hi x8 | lo x8] of T (all threads; a barrier
   // publishes it)
-  auto convert = [&](int bf) __attribute__((always_inline)) {
+  auto convert = [&]() __attribute__((always_inline)) {
     for (int v = tid; v < kP * (N / 8); v += kThreads) {
       const int row = v / (N / 8), q = v % (N / 8);
-      float* ph_ = &ss[bf][row * N + 4 * ((2 * q) ^ (row & 7))];
-      float* pl_ = &ss[bf][row * N + 4 * ((2 * q + 1) ^ (row & 7))];
+      float* ph_ = &ss[row * N + 4 * ((2 * q) ^ (row & 7))];
+      float* pl_ = &ss[row * N + 4 * ((2 * q + 1) ^ (row & 7))];
       const f32x4 v0 = *reinterpret_cast<const f32x4*>(ph_);
       const f32x4 v1 = *reinterpret_cast<const f32x4*>(pl_);
       frag8<T> hi, lo;
@@ -135,9 +141,9 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
   issue_head(h0, 0);
   // B rows of the chunk (N elements of T, piece k of row s at slot k ^ (s %
   // BPR) so that the 16 rows one C.B^T operand read takes hit distinct banks)
-  // into S_in's second buffer, free until the first head issues the second
-  // head's copies (Q N 2 <= kP N 4 bytes)
-  const uint32_t bt_lds = ss_lds + kP * N * 4;
+  // into S_in's buffer, free until the first head's S_in is copied
+  // (Q N 2 <= kP N 4 bytes)
+  const uint32_t bt_lds = ss_lds;
 #pragma unroll
   for (int m = 0; m < BPW; ++m) {
     const int blk = wave + kNW * m, r = blk * (64 / BPR) + lane / BPR, pc = (lane % BPR) ^ (r % BPR);
@@ -152,7 +158,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
     for (int kc = 0; kc < NK; ++kc) cf[r][kc] = load8<T>(cg + (16 * trow[r] + i) * p.scl + 32 * kc + 8 * g);
   dma_wait();
   __syncthreads();
-  const T* bt = reinterpret_cast<const T*>(&ss[1][0]);
+  const T* bt = reinterpret_cast<const T*>(&ss[0]);
   // cbr[r][sb][st][jj] = C.B^T[s = 32 sb + 16 st + 4 g + jj][l = 16 t + i]
   f32x4 cbr[RT][NSB][2];
 #pragma unroll
@@ -174,8 +180,11 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
         cbr[r][sb][st] = d;
       }
   }
-  __syncthreads();  // B's buffer takes the second head's copies from here on
-  convert(0);
+  __syncthreads();  // B's buffer takes the first head's S_in from here on
+  issue_sin(h0);
+  dma_wait();
+  __syncthreads();
+  convert();
   __syncthreads();
 
   // x^T operand of p tile pt (via ds_read_b64_tr_b16): rows 4 g + i / 4
@@ -211,7 +220,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
     if (h + 1 < h1) issue_head(h + 1, bf ^ 1);
     hprev = h;
     const T* xb = xs[bf];
-    const T* sb_ = reinterpret_cast<const T*>(&ss[bf][0]);
+    const T* sb_ = reinterpret_cast<const T*>(&ss[0]);
     const float* ab = al[bf];
 
     // ---- off-diagonal: acc[p, l] = exp(Acs[l]) sum_n S_in[p, n] C[l, n] ----
@@ -235,6 +244,9 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
           acc[r][e] = mma(lo, cf[r][kc], acc[r][e]);
         }
       }
+    // every wave is done with S_in: the next head's comes in under the diagonal
+    __syncthreads();
+    if (h + 1 < h1) issue_sin(h + 1);
     // log2(e) Acs[l] of this lane's token l = 16 t + i in each row tile
     float all[RT];
 #pragma unroll
@@ -290,7 +302,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
     dma_wait();
     __syncthreads();
     if (h + 1 < h1) {
-      convert(bf ^ 1);
+      convert();
       __syncthreads();
     }
   }
