@@ -16,10 +16,11 @@ Kernels per shape: C3, C4 and the R0 layer span (16-bit, chunk 256) run
 chunk_prep, the persistent chunk_state / chunk_scan and the state chain; C2
 and C5 (f32, chunk 64 / 128) the f32 chunk_scan, chunk_state and chain, and
 R0's core (16-bit inputs at chunk 64) the same chunk_state and chain on
-16-bit staged rows; every shape runs state_passing.  C1 (d_state 16) and R0's
-chunk_scan run the generic kernels, whose staging loops bound every row and
-column by the shape explicitly (ssd_device.h stage_rows / stage_transposed)
-instead of by lane arithmetic.
+16-bit staged rows and the 16-bit chunk_scan for f32 states (also checked at
+chunk 128, d_state 64); every shape runs state_passing.  C1 (d_state 16) runs
+the generic kernels, whose staging loops bound every row and column by the
+shape explicitly (ssd_device.h stage_rows / stage_transposed) instead of by
+lane arithmetic.
 
 The restatements are pinned to the source: each check first asserts that
 the lines it restates still read as below in the kernel file
@@ -499,6 +500,95 @@ def test_f32_kernel_addresses(name):
     n = np.arange(N // 64)[None, :, None, None]
     inside("state rows", 16 * (2 * pp + a) + i, 0, P)
     inside("state columns", 16 * (nt0 + n) + 4 * g + 3, 0, N)
+
+
+# ---------------------------------------------------------------------------
+# chunk_scan for 16-bit inputs with f32 states (ssd_chunk_scan_b16.hip)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("Q,N", [(64, 128), (64, 64), (128, 64)])
+def test_chunk_scan_b16_addresses(Q, N):
+    P, RT = 64, Q // 64
+    pin("ssd_chunk_scan_b16.hip",
+        "constexpr int XPW = Q * kP * 2 / 1024 / kNW;",
+        "constexpr int SPW = kP * N / 256 / kNW;",
+        "constexpr int BPR = N * 2 / 16;",
+        "constexpr int BPW = Q * N * 2 / 1024 / kNW;",
+        "__shared__ __attribute__((aligned(1024))) T xs[2][Q * kP];",
+        "__shared__ __attribute__((aligned(1024))) float ss[kP * N];",
+        "const int64_t xcopy = (int64_t)(lane >> 3) * p.sxl + 8 * ((lane & 7) ^ (lane >> 3));",
+        "dma16_at(xg + (int64_t)(8 * blk) * p.sxl, xs_lds + (uint32_t)((bf * Q * kP) * 2 + blk * 1024));",
+        "const int blk = wave + kNW * m, r = blk * (64 / SPR) + lane / SPR, pc = (lane % SPR) ^ (r & 7);",
+        "dma16_at(sg + r * N + 4 * pc, ss_lds + (uint32_t)(blk * 1024));",
+        "const int row = v / (N / 8), q = v % (N / 8);",
+        "const int blk = wave + kNW * m, r = blk * (64 / BPR) + lane / BPR, pc = (lane % BPR) ^ (r % BPR);",
+        "dma16_at(bg + r * p.sbl + 8 * pc, bt_lds + (uint32_t)(blk * 1024));",
+        "const frag8<T> bf8 = *reinterpret_cast<const frag8<T>*>(bt + row * N + 8 * ((4 * kc + g) ^ (row % BPR)));",
+        "cf[r][kc] = load8<T>(cg + (16 * trow[r] + i) * p.scl + 32 * kc + 8 * g);",
+        "for (int e = 0; e < 2; ++e) xoff[e] = r * kP + 8 * ((2 * (2 * ph + e) + ((i & 3) >> 1)) ^ x7) + 4 * (i & 1);",
+        "const T* a0 = xb + xoff[e] + (32 * sb) * kP;",
+        "const int row = 16 * (2 * ph + e) + i, q = 4 * kc + g;",
+        "const frag8<T> hi = *reinterpret_cast<const frag8<T>*>(srow + 8 * ((2 * q) ^ (row & 7)));",
+        "const frag8<T> lo = *reinterpret_cast<const frag8<T>*>(srow + 8 * ((2 * q + 1) ^ (row & 7)));",
+        "*reinterpret_cast<vec4<T>*>(yg + (int64_t)(16 * trow[r] + i) * p.syl + 16 * (2 * ph + e) + 4 * g) = o;",
+        "const int ph = wave >> 2, rg = RT == 1 && ph ? 3 - (wave & 3) : wave & 3;")
+    wave, lane = lanes()
+    g, i = lane >> 4, lane & 15
+    # x copies: 1 KB blocks of 8 rows of 64 16-bit elements
+    xpw = Q * P * 2 // 1024 // 8
+    blk = wave + 8 * np.arange(xpw)[:, None, None]
+    xr = 8 * blk + (lane >> 3)
+    inside("x rows", xr, 0, Q)
+    inside("x elements", 8 * ((lane & 7) ^ (lane >> 3)) + 7, 0, P)
+    inside("x LDS (2 buffers)", 1 * Q * P * 2 + blk * 1024 + 16 * lane + 15, 0, 2 * Q * P * 2)
+    # S_in copies (f32 rows of N floats)
+    spr = N // 4
+    spw = P * N // 256 // 8
+    sblk = wave + 8 * np.arange(spw)[:, None, None]
+    sr = sblk * (64 // spr) + lane // spr
+    inside("S_in rows", sr, 0, P)
+    inside("S_in floats", 4 * ((lane % spr) ^ (sr & 7)) + 3, 0, N)
+    inside("S_in LDS", sblk * 1024 + 16 * lane + 15, 0, P * N * 4)
+    # in-place conversion: pair q of row `row`, pieces (2 q) ^ (row & 7) and (2 q + 1) ^ (row & 7)
+    v = np.arange(P * (N // 8))
+    row, q = v // (N // 8), v % (N // 8)
+    inside("S_in convert floats", 4 * np.maximum((2 * q) ^ (row & 7), (2 * q + 1) ^ (row & 7)) + 3, 0, N)
+    # B copies (N 16-bit elements per row, BPR pieces) into S_in's buffer
+    bpr = N * 2 // 16
+    bpw = Q * N * 2 // 1024 // 8
+    bblk = wave + 8 * np.arange(bpw)[:, None, None]
+    br = bblk * (64 // bpr) + lane // bpr
+    inside("B rows", br, 0, Q)
+    inside("B elements", 8 * ((lane % bpr) ^ (br % bpr)) + 7, 0, N)
+    inside("B LDS (in S_in's buffer)", bblk * 1024 + 16 * lane + 15, 0, P * N * 4)
+    # C.B^T operand reads: rows 32 sb + 16 st + i < Q, pieces (4 kc + g) ^ (row % BPR)
+    kc = np.arange(N // 32)[:, None, None, None]
+    rowb = 32 * np.arange(2 * RT)[:, None, None] + 16 * np.arange(2)[:, None] + i
+    inside("C.B^T B rows", rowb, 0, Q)
+    inside("C.B^T B elements", 8 * ((4 * kc + g.reshape(1, 1, 1, 64)) ^ (rowb[None] % bpr)) + 7, 0, N)
+    # C fragments and y stores: rows 16 t + i, t from the wave's row group
+    ph = wave >> 2
+    rg = np.where((RT == 1) & (ph > 0), 3 - (wave & 3), wave & 3)
+    trow = [rg] + ([7 - rg] if RT == 2 else [])
+    for t in trow:
+        inside("C / y rows", 16 * t + i, 0, Q)
+    inside("C columns", 32 * kc + 8 * g + 7, 0, N)
+    inside("y columns", 16 * (2 * ph + np.arange(2)[:, None, None]) + 4 * g + 3, 0, P)
+    # S_in hi / lo operand reads (16-bit slots of the f32 rows: 2 N per row)
+    e_ = np.arange(2)[:, None, None, None]
+    srow_ = 16 * (2 * ph[..., None] + e_) + i[..., None]
+    qq = 4 * np.arange(N // 32)[:, None, None, None, None] + g[..., None]
+    inside("S_in operand rows", srow_, 0, P)
+    inside("S_in operand elements", 8 * ((2 * qq + 1) ^ (srow_ & 7)) + 7, 0, 2 * N)
+    # x^T operand reads (ds_read_b64_tr_b16, 4 elements): rows 4 g + i / 4 + 16 h + 32 sb,
+    # columns 8 ((2 pt + (i & 3) / 2) ^ (row & 7)) + 4 (i & 1) .. + 3
+    r4 = 4 * g + (i >> 2)
+    pt = 2 * ph[..., None] + e_
+    col = 8 * ((2 * pt + ((i & 3) >> 1)) ^ (r4 & 7)) + 4 * (i & 1)
+    inside("x^T columns", col + 3, 0, P)
+    inside("x^T rows", r4 + 16 + 32 * (2 * RT - 1), 0, Q)
+    # the LDS arrays: x 2 buffers, S_in one buffer (B staged in it: Q N 2 <= P N 4)
+    assert Q * N * 2 <= P * N * 4
 
 
 # ---------------------------------------------------------------------------
