@@ -63,6 +63,31 @@ __device__ __forceinline__ float chunk_weight(float acs_l, float last_log2, floa
   return __builtin_amdgcn_exp2f(__builtin_fmaf(acs_l, -kLog2e, last_log2)) * dt_l;
 }
 
+// The B operand fragments as the MFMA takes them: f32 values for f32 inputs,
+// the inputs' own 16-bit values otherwise.
+template <typename T> using BFrag = typename std::conditional<std::is_same<T, float>::value, frag8<float>, frag8<T>>::type;
+
+// One K step of S^T += B^T (w x) for one p tile: x is this lane's 8 tokens of
+// column p (K slots in the B fragment's order) and w their weights.  f32
+// inputs: the f32 products on 16x16x4 f32 MFMAs.  16-bit inputs: the
+// weighted x split into a hi + lo pair of the input type (hi = round(x w),
+// lo = round(x w - hi), ~16 significant bits through the MFMA) on two
+// 16x16x32 MFMAs of that type, B exact.
+template <typename T>
+__device__ __forceinline__ f32x4 kstep(const BFrag<T>& bf, const frag8<T>& x, const float* w, f32x4 acc) {
+  if constexpr (std::is_same<T, float>::value) {
+    frag8<float> xf;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) xf[j] = x[j] * w[j];
+    return mma(bf, xf, acc);
+  } else {
+    frag8<T> hi, lo;
+    split_weighted<T>(x, f32x4{w[0], w[1], w[2], w[3]}, f32x4{w[4], w[5], w[6], w[7]}, hi, lo);
+    acc = mma(bf, hi, acc);
+    return mma(bf, lo, acc);
+  }
+}
+
 template <typename T, int NK, int RT, bool HAS_DT>
 __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArgs p, int hs, int slices) {
   constexpr int Q = 64 * RT;
@@ -121,7 +146,7 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
   for (int m = 0; m < BPW; ++m) stage_rows<T>(bg, p.sbl, N, wave + kNW * m, lds_base + (uint32_t)(Q * kP * ES), lane);
   dma_wait();
   __syncthreads();
-  frag8<float> bfr[NTW][KS];
+  BFrag<T> bfr[NTW][KS];
   {
     const T* bl = lds + Q * kP;
 #pragma unroll
@@ -130,7 +155,7 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
       for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          bfr[n][ks][j] = to_f32<T>(bl[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)]);
+          bfr[n][ks][j] = bl[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)];
   }
   __syncthreads();  // B's LDS is x buffer 1 from here on
 
@@ -178,11 +203,11 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int col = 16 * (2 * pp + a) + i;
-        frag8<float> xf;
+        frag8<T> xr;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xf[j] = to_f32<T>(xb[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)]) * w[j];
+        for (int j = 0; j < 8; ++j) xr[j] = xb[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)];
 #pragma unroll
-        for (int n = 0; n < NTW; ++n) acc[a][n] = mma(bfr[n][ks], xf, acc[a][n]);
+        for (int n = 0; n < NTW; ++n) acc[a][n] = kstep<T>(bfr[n][ks], xr, w, acc[a][n]);
       }
     }
     dma_wait();
@@ -316,20 +341,20 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
 #pragma unroll
         for (int jj = 0; jj < 4; ++jj) w[4 * s2 + jj] = chunk_weight(a4[jj], last, d4[jj]);
       }
-      frag8<float> bfr[NTW];
+      BFrag<T> bfr[NTW];
 #pragma unroll
       for (int n = 0; n < NTW; ++n)
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          bfr[n][j] = to_f32<T>(bl[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)]);
+          bfr[n][j] = bl[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)];
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int col = 16 * (2 * pp + a) + i;
-        frag8<float> xf;
+        frag8<T> xr;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xf[j] = to_f32<T>(xb[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)]) * w[j];
+        for (int j = 0; j < 8; ++j) xr[j] = xb[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)];
 #pragma unroll
-        for (int n = 0; n < NTW; ++n) acc[a][n] = mma(bfr[n], xf, acc[a][n]);
+        for (int n = 0; n < NTW; ++n) acc[a][n] = kstep<T>(bfr[n], xr, w, acc[a][n]);
       }
     }
     // the recurrence (state_passing's f32 FMA)
