@@ -1,8 +1,9 @@
 // K2 -- chunk_state for f32 states at chunk 64 / 128 and d_state 64 / 128
 // (the Mamba-2-130M shape, the grouped short-sequence shape, and MR's own
 // block_len 64 with 16-bit inputs).  Inputs of type T (f32, bf16 or f16) are
-// staged as they are and converted exactly to f32 as the operands are read,
-// so every product is an f32 MFMA on the inputs' exact values.  Same result
+// staged as they are.  f32 inputs: every product is an f32 MFMA on the
+// inputs' exact values.  16-bit inputs: 16x16x32 MFMAs of the input type,
+// B exact and the weighted x as a hi + lo pair (kstep below).  Same result
 // as the generic kernel in ssd_chunk_state.hip up to its 16-bit rounding of
 // the weighted operand (workloads/mamba/model_ref.py:144, 148-149):
 //   S[p, n] = sum_l (w[l] x[l, p]) B[l, n],   w[l] = exp(Acs[Q-1] - Acs[l]) dt[l]
@@ -14,8 +15,8 @@
 // registers for all of them; per head only x (and Acs, dt) move, copied
 // global -> LDS one head ahead (global_load_lds, rows XOR-swizzled by 16-byte
 // piece so the column reads of the A operand are free of bank conflicts).
-// The weight w[l] is applied in f32 as the A operand is read: no rounding
-// beyond f32's.
+// The weight w[l] is applied in f32 as the x operand is read (for 16-bit
+// inputs the product is then split into the hi + lo pair).
 //
 // Work decomposition: 8 waves; wave w owns p tiles 2 (w % 2), 2 (w % 2) + 1
 // and n tiles [(w / 2) N / 64, (w / 2 + 1) N / 64).  K index slot (g, j) of

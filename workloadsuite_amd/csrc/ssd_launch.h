@@ -194,9 +194,10 @@ hipError_t launch_chunk_scan_persistent(const ChunkScanArgs& a, int dtype, int s
 // without the layer epilogue (ssd_chunk_scan_f32.hip): C.B^T once per
 // (b, c, group); launch_chunk_scan dispatches to it when supported.
 bool chunk_scan_f32_supported(const ChunkScanArgs& a, int dtype, int state_dtype);
-// chunk_state for f32 states at chunk 64 / 128, d_state 64 / 128, f32 MFMAs
-// on inputs of any type (ssd_chunk_state_f32.hip): B once per (b, c, group);
-// launch_chunk_state dispatches to it when supported.
+// chunk_state for f32 states at chunk 64 / 128, d_state 64 / 128, f32 or
+// 16-bit inputs (ssd_chunk_state_f32.hip: f32 MFMAs, or 16-bit MFMAs with the
+// weighted x as hi/lo pairs): B once per (b, c, group); launch_chunk_state
+// dispatches to it when supported.
 bool chunk_state_f32_supported(const ChunkStateArgs& a, int dtype, int state_dtype);
 hipError_t launch_chunk_state_f32(const ChunkStateArgs& a, int dtype, hipStream_t stream);
 // ... and K2 + K3 as one launch for f32 states (one workgroup per (b, h)
