@@ -380,12 +380,15 @@ template <typename T, int NK, int RT>
 hipError_t launch_chain_qn(const ChunkStateArgs& a, const StatePassingArgs& sp, hipStream_t stream) {
   const int64_t chains = (int64_t)a.batch * a.nheads;
   if (chains > INT32_MAX) return hipErrorInvalidValue;
-  // two chunks of x and B in LDS (one workgroup per CU) while chains are
-  // fewer than two per CU; with more, one chunk (two workgroups per CU, each
-  // covering the other's copy latency): C2 (192 chains of 32 chunks) 7%
-  // faster double-buffered, C5 (4096 chains of 4) 3% faster single-buffered
+  // two chunks of x and B in LDS (one workgroup per CU at f32) while chains
+  // are fewer than two per CU; with more, one chunk (two workgroups per CU,
+  // each covering the other's copy latency): C2 (192 chains of 32 chunks) 7%
+  // faster double-buffered, C5 (4096 chains of 4) 3% faster single-buffered.
+  // 16-bit inputs always double-buffer: their two chunks (48 KB at chunk 64,
+  // d_state 128) still leave room for two workgroups per CU (R0's core, 1024
+  // chains of 32 chunks: 404 -> 378 us)
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
-  const bool db = chains < 2 * (int64_t)cus;
+  const bool db = chains < 2 * (int64_t)cus || !std::is_same<T, float>::value;
   auto kern = db ? (a.dt ? chunk_state_chain_f32_kernel<T, NK, RT, true, true> : chunk_state_chain_f32_kernel<T, NK, RT, false, true>)
                  : (a.dt ? chunk_state_chain_f32_kernel<T, NK, RT, true, false> : chunk_state_chain_f32_kernel<T, NK, RT, false, false>);
   kern<<<dim3((unsigned)chains), dim3(kThreads), 0, stream>>>(a, sp);
