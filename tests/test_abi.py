@@ -77,7 +77,9 @@ def test_workspace_bytes_layout():
     bhc = 2 * 8 * 4
     states32 = bhc * 64 * 64 * 4
     assert n32 >= bhc * 64 * 4 + bhc * 4 + states32 and n32 % 256 == 0
-    assert n32 - n16 == states32 // 2
+    # f32 states also carry the f16s hand-over's row scales ([b, c, h, P] f32,
+    # read by the 16-bit chunk_scan at chunk 64 / 128)
+    assert n32 - n16 == states32 // 2 + bhc * 64 * 4
     bad = d(seqlen=100)
     assert lib.ssd_workspace_bytes(ctypes.byref(bad), _lib.DTYPE_F32) == 0
     # chunk 256, dstate 128: also chunk_prep's CB^T fragments (8 waves x 9 steps

@@ -422,7 +422,14 @@ def test_f32_kernel_addresses(name):
         "*reinterpret_cast<f32x4*>(sg + sidx(a, n)) = st[a][n];",
         "*reinterpret_cast<const f32x4*>(sp.init + bh * PN + sidx(a, n))",
         "*reinterpret_cast<f32x4*>(sp.final_state + bh * PN + sidx(a, n)) = st[a][n];",
-        "const int pp = wave & 1, nt0 = (wave >> 1) * NTW;")
+        "const int pp = wave & 1, nt0 = (wave >> 1) * NTW;",
+        "__shared__ float rmax[F16S ? 2 : 1][F16S ? 4 * kP : 1];",
+        "if (g == 0) rmax[buf][(wave >> 1) * kP + 16 * (2 * pp + a) + i] = m;",
+        "const float* rm = rmax[c & 1];",
+        "const int pr = 16 * (2 * pp + a) + i;",
+        "const float m = fmaxf(fmaxf(rm[pr], rm[kP + pr]), fmaxf(rm[2 * kP + pr], rm[3 * kP + pr]));",
+        "*reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(sg + pr * N) + 16 * (nt0 + n) + 4 * g) = hv;",
+        "sp.sscale[(((int64_t)b * p.nchunks + c) * p.nheads + h) * kP + pr] = __builtin_ldexpf(1.f, e);")
     wave, lane = lanes()
     g, i = lane >> 4, lane & 15
     # x copies (chunk_scan, chunk_state, chain): 1 KB = 4 rows of 64 floats
@@ -500,27 +507,51 @@ def test_f32_kernel_addresses(name):
     n = np.arange(N // 64)[None, :, None, None]
     inside("state rows", 16 * (2 * pp + a) + i, 0, P)
     inside("state columns", 16 * (nt0 + n) + 4 * g + 3, 0, N)
+    # the chain's f16s S_in (16-bit inputs): 4 f16 at f16 column 16 (nt0 + n)
+    # + 4 g of row pr, inside the row's first half (2 N bytes of its 4 N);
+    # row maxima: quarter wave / 2 of row pr, every (quarter, row) written
+    # by exactly one lane (g == 0) and the 4 quarters read for each row
+    pr = 16 * (2 * pp + a) + i
+    inside("f16s S_in f16 columns", 16 * (nt0 + n) + 4 * g + 3, 0, N)
+    slots = ((wave >> 1) * P + pr)[..., :16]                   # the lanes with g == 0
+    assert sorted(slots.ravel().tolist()) == list(range(4 * P))
+    inside("row maxima read", 3 * P + pr, 0, 4 * P)
+    inside("row scale (quarter 0, g == 0)", pr, 0, P)
 
 
 # ---------------------------------------------------------------------------
 # chunk_scan for 16-bit inputs with f32 states (ssd_chunk_scan_b16.hip)
 # ---------------------------------------------------------------------------
 
+@pytest.mark.parametrize("f16s", [False, True])
 @pytest.mark.parametrize("Q,N", [(64, 128), (64, 64), (128, 64)])
-def test_chunk_scan_b16_addresses(Q, N):
+def test_chunk_scan_b16_addresses(Q, N, f16s):
+    """f16s: S_in as f16 rows (the first half of each f32 row) with a scale
+    per row, read as they lie; otherwise f32 rows split in LDS into hi / lo
+    pairs.  Either way S_in's buffer first stages the chunk's B rows."""
     P, RT = 64, Q // 64
     pin("ssd_chunk_scan_b16.hip",
+        "constexpr int SRB = F16S ? N * 2 : N * 4;",
+        "constexpr int SPR = SRB / 16;",
         "constexpr int XPW = Q * kP * 2 / 1024 / kNW;",
-        "constexpr int SPW = kP * N / 256 / kNW;",
+        "constexpr int SPW = kP * SRB / 1024 / kNW;",
         "constexpr int BPR = N * 2 / 16;",
         "constexpr int BPW = Q * N * 2 / 1024 / kNW;",
+        "constexpr int SSB = kP * SRB > Q * N * 2 ? kP * SRB : Q * N * 2;",
         "__shared__ __attribute__((aligned(1024))) T xs[2][Q * kP];",
-        "__shared__ __attribute__((aligned(1024))) float ss[kP * N];",
+        "__shared__ __attribute__((aligned(1024))) float ss[SSB / 4];",
+        "__shared__ __attribute__((aligned(16))) float scl[F16S ? kP : 4];",
         "const int64_t xcopy = (int64_t)(lane >> 3) * p.sxl + 8 * ((lane & 7) ^ (lane >> 3));",
         "dma16_at(xg + (int64_t)(8 * blk) * p.sxl, xs_lds + (uint32_t)((bf * Q * kP) * 2 + blk * 1024));",
-        "const int blk = wave + kNW * m, r = blk * (64 / SPR) + lane / SPR, pc = (lane % SPR) ^ (r & 7);",
-        "dma16_at(sg + r * N + 4 * pc, ss_lds + (uint32_t)(blk * 1024));",
+        "if constexpr (!F16S) return r & 7;",
+        "else if constexpr (SPR >= 16) return r & 15;",
+        "else return (r >> 1) & 7;",
+        "const int blk = wave + kNW * m, r = blk * (64 / SPR) + lane / SPR, pc = (lane % SPR) ^ ssw(r);",
+        "dma16_at(sg + r * (N * 4) + 16 * pc, ss_lds + (uint32_t)(blk * 1024));",
+        "if (wave == 0) dma4_at(p.sscale + item * kP + lane, scl_lds);",
         "const int row = v / (N / 8), q = v % (N / 8);",
+        "float* ph_ = &ss[row * N + 4 * ((2 * q) ^ (row & 7))];",
+        "float* pl_ = &ss[row * N + 4 * ((2 * q + 1) ^ (row & 7))];",
         "const int blk = wave + kNW * m, r = blk * (64 / BPR) + lane / BPR, pc = (lane % BPR) ^ (r % BPR);",
         "dma16_at(bg + r * p.sbl + 8 * pc, bt_lds + (uint32_t)(blk * 1024));",
         "const frag8<T> bf8 = *reinterpret_cast<const frag8<T>*>(bt + row * N + 8 * ((4 * kc + g) ^ (row % BPR)));",
@@ -528,12 +559,23 @@ def test_chunk_scan_b16_addresses(Q, N):
         "for (int e = 0; e < 2; ++e) xoff[e] = r * kP + 8 * ((2 * (2 * ph + e) + ((i & 3) >> 1)) ^ x7) + 4 * (i & 1);",
         "const T* a0 = xb + xoff[e] + (32 * sb) * kP;",
         "const int row = 16 * (2 * ph + e) + i, q = 4 * kc + g;",
-        "const frag8<T> hi = *reinterpret_cast<const frag8<T>*>(srow + 8 * ((2 * q) ^ (row & 7)));",
-        "const frag8<T> lo = *reinterpret_cast<const frag8<T>*>(srow + 8 * ((2 * q + 1) ^ (row & 7)));",
+        "const unsigned char* srow = sb_ + row * SRB;",
+        "const f16x8 a = *reinterpret_cast<const f16x8*>(srow + 16 * (q ^ ssw(row)));",
+        "const frag8<T> hi = *reinterpret_cast<const frag8<T>*>(srow + 16 * ((2 * q) ^ ssw(row)));",
+        "const frag8<T> lo = *reinterpret_cast<const frag8<T>*>(srow + 16 * ((2 * q + 1) ^ ssw(row)));",
+        "for (int e = 0; e < 2; ++e) sc[e] = *reinterpret_cast<const f32x4*>(&scl[16 * (2 * ph + e) + 4 * g]);",
         "*reinterpret_cast<vec4<T>*>(yg + (int64_t)(16 * trow[r] + i) * p.syl + 16 * (2 * ph + e) + 4 * g) = o;",
         "const int ph = wave >> 2, rg = RT == 1 && ph ? 3 - (wave & 3) : wave & 3;")
     wave, lane = lanes()
     g, i = lane >> 4, lane & 15
+    srb = 2 * N if f16s else 4 * N          # bytes of an S_in row in LDS
+    spr = srb // 16
+    ssb = max(P * srb, Q * N * 2)            # S_in's buffer, which also stages B
+
+    def ssw(r):
+        if not f16s:
+            return r & 7
+        return r & 15 if spr >= 16 else (r >> 1) & 7
     # x copies: 1 KB blocks of 8 rows of 64 16-bit elements
     xpw = Q * P * 2 // 1024 // 8
     blk = wave + 8 * np.arange(xpw)[:, None, None]
@@ -541,18 +583,25 @@ def test_chunk_scan_b16_addresses(Q, N):
     inside("x rows", xr, 0, Q)
     inside("x elements", 8 * ((lane & 7) ^ (lane >> 3)) + 7, 0, P)
     inside("x LDS (2 buffers)", 1 * Q * P * 2 + blk * 1024 + 16 * lane + 15, 0, 2 * Q * P * 2)
-    # S_in copies (f32 rows of N floats)
-    spr = N // 4
-    spw = P * N // 256 // 8
+    # S_in copies: rows of srb bytes (f16s: the f16 half of each 4 N-byte row)
+    spw = P * srb // 1024 // 8
+    assert spw >= 1
     sblk = wave + 8 * np.arange(spw)[:, None, None]
     sr = sblk * (64 // spr) + lane // spr
     inside("S_in rows", sr, 0, P)
-    inside("S_in floats", 4 * ((lane % spr) ^ (sr & 7)) + 3, 0, N)
-    inside("S_in LDS", sblk * 1024 + 16 * lane + 15, 0, P * N * 4)
-    # in-place conversion: pair q of row `row`, pieces (2 q) ^ (row & 7) and (2 q + 1) ^ (row & 7)
-    v = np.arange(P * (N // 8))
-    row, q = v // (N // 8), v % (N // 8)
-    inside("S_in convert floats", 4 * np.maximum((2 * q) ^ (row & 7), (2 * q + 1) ^ (row & 7)) + 3, 0, N)
+    inside("S_in pieces", (lane % spr) ^ ssw(sr), 0, spr)
+    inside("S_in bytes of the row", 16 * ((lane % spr) ^ ssw(sr)) + 15, 0, srb)
+    inside("S_in LDS", sblk * 1024 + 16 * lane + 15, 0, ssb)
+    assert P * srb == 1024 * 8 * spw            # the copies cover every row once
+    if f16s:
+        inside("S_in row scales (wave 0)", lane, 0, P)
+    else:
+        # in-place conversion: pair q of row `row`, pieces (2 q) ^ (row & 7) and (2 q + 1) ^ (row & 7)
+        v = np.arange(P * (N // 8))
+        row, q = v // (N // 8), v % (N // 8)
+        inside("S_in convert floats", row * N + 4 * np.maximum((2 * q) ^ (row & 7), (2 * q + 1) ^ (row & 7)) + 3,
+               0, P * N)
+        assert (ssw(row) == (row & 7)).all()       # the copies' swizzle
     # B copies (N 16-bit elements per row, BPR pieces) into S_in's buffer
     bpr = N * 2 // 16
     bpw = Q * N * 2 // 1024 // 8
@@ -560,7 +609,7 @@ def test_chunk_scan_b16_addresses(Q, N):
     br = bblk * (64 // bpr) + lane // bpr
     inside("B rows", br, 0, Q)
     inside("B elements", 8 * ((lane % bpr) ^ (br % bpr)) + 7, 0, N)
-    inside("B LDS (in S_in's buffer)", bblk * 1024 + 16 * lane + 15, 0, P * N * 4)
+    inside("B LDS (in S_in's buffer)", bblk * 1024 + 16 * lane + 15, 0, ssb)
     # C.B^T operand reads: rows 32 sb + 16 st + i < Q, pieces (4 kc + g) ^ (row % BPR)
     kc = np.arange(N // 32)[:, None, None, None]
     rowb = 32 * np.arange(2 * RT)[:, None, None] + 16 * np.arange(2)[:, None] + i
@@ -574,12 +623,22 @@ def test_chunk_scan_b16_addresses(Q, N):
         inside("C / y rows", 16 * t + i, 0, Q)
     inside("C columns", 32 * kc + 8 * g + 7, 0, N)
     inside("y columns", 16 * (2 * ph + np.arange(2)[:, None, None]) + 4 * g + 3, 0, P)
-    # S_in hi / lo operand reads (16-bit slots of the f32 rows: 2 N per row)
+    # S_in operand reads: f16s piece q, else the hi / lo pieces 2 q, 2 q + 1
     e_ = np.arange(2)[:, None, None, None]
     srow_ = 16 * (2 * ph[..., None] + e_) + i[..., None]
     qq = 4 * np.arange(N // 32)[:, None, None, None, None] + g[..., None]
     inside("S_in operand rows", srow_, 0, P)
-    inside("S_in operand elements", 8 * ((2 * qq + 1) ^ (srow_ & 7)) + 7, 0, 2 * N)
+    piece = qq ^ ssw(srow_) if f16s else np.maximum((2 * qq) ^ ssw(srow_), (2 * qq + 1) ^ ssw(srow_))
+    inside("S_in operand bytes", 16 * piece + 15, 0, srb)
+    if f16s:
+        # the 16 lanes of one read (one g) hit 16 distinct 16-byte bank slots
+        slot = (((srow_ * srb + 16 * (qq ^ ssw(srow_))) % 256) // 16)[..., 0]   # [kc, e, wave, lane]
+        for k in range(slot.shape[0]):
+            for e in range(2):
+                for gg in range(4):
+                    got = slot[k, e, :, 16 * gg:16 * gg + 16]
+                    assert all(len(set(r.tolist())) == 16 for r in got), (k, e, gg)
+        inside("row scale reads", 16 * (2 * ph + np.arange(2)[:, None, None]) + 4 * g + 3, 0, P)
     # x^T operand reads (ds_read_b64_tr_b16, 4 elements): rows 4 g + i / 4 + 16 h + 32 sb,
     # columns 8 ((2 pt + (i & 3) / 2) ^ (row & 7)) + 4 (i & 1) .. + 3
     r4 = 4 * g + (i >> 2)
@@ -587,8 +646,6 @@ def test_chunk_scan_b16_addresses(Q, N):
     col = 8 * ((2 * pt + ((i & 3) >> 1)) ^ (r4 & 7)) + 4 * (i & 1)
     inside("x^T columns", col + 3, 0, P)
     inside("x^T rows", r4 + 16 + 32 * (2 * RT - 1), 0, Q)
-    # the LDS arrays: x 2 buffers, S_in one buffer (B staged in it: Q N 2 <= P N 4)
-    assert Q * N * 2 <= P * N * 4
 
 
 # ---------------------------------------------------------------------------

@@ -222,6 +222,32 @@ def test_k4_chunk_scan(dtype, Q, N):
     assert_close(Y, Y_ref, tolerance(dtype))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Q,N,use_dt,init", [(64, 128, True, True), (64, 64, False, False), (128, 64, True, False)])
+def test_k4_f16s_states_at_chunk_64_128(dtype, Q, N, use_dt, init):
+    """chunk_scan on S_in handed over as "f16s" (f16 rows, a power-of-two
+    scale per row) at chunk 64 / 128, where the 16-bit kernel reads them: the
+    y of chunk_scan on the same states decoded to f32 (C rounded to f16 with
+    a power-of-two scale per row is exact for these inputs, so only the f32
+    summation order differs: one rounding of the output type), and the
+    oracle's within the 16-bit tolerance.  Groups of 4 heads over 2 head
+    slices, 5 chunks."""
+    say("k4 f16s", dtype, Q, N, use_dt, init)
+    cfg, inp = small_case(dtype, Q, N, b=2, nc=5, h=8, g=2, init=init)
+    d = to_dev(inp)
+    dt = torch.rand(2, 5 * Q, 8, generator=torch.Generator().manual_seed(5)) + 0.5 if use_dt else None
+    dtd = None if dt is None else dt.to(DEV)
+    Acs, dec = S.chunk_cumsum(d["A"], Q)
+    st = S.chunk_state(d["X"], d["B"], Acs, dt=dtd)
+    S_f, _ = S.state_passing(st, dec, d["init"], split="f16s")
+    Yf = S.chunk_scan(d["X"], d["B"], d["C"], Acs, S_f, dt=dtd, split="f16s")
+    Yd = S.chunk_scan(d["X"], d["B"], d["C"], Acs, S_f.decode(), dt=dtd)
+    eps = 2.0 ** -8 if dtype == torch.bfloat16 else 2.0 ** -11
+    assert_close(Yf, Yd.float(), eps, atol=eps * Yd.float().abs().max().item())
+    Ys, _ = O.ssd_sequential(inp["X"], inp["A"], inp["B"], inp["C"], dt=dt, initial_states=inp["init"])
+    assert_close(Yf, Ys, tolerance(dtype))
+
+
 @pytest.mark.parametrize("Q", [64, 256])
 def test_k4_masked_exponent_is_never_evaluated(Q):
     """A = -4|N(0,1)|: every causal decay exp(Acs[l]-Acs[s]), s <= l, is <= 1,

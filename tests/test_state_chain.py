@@ -204,3 +204,48 @@ def test_f32_forward_equals_kernels_one_by_one(b, L, h, N, g, Q):
     torch.cuda.synchronize()
     assert torch.equal(final, fk)
     assert torch.equal(Y, Yk)
+
+
+def _f16_halves(s):
+    """The f16 values of f16s states (the first half of each f32 row)."""
+    return s.states.view(torch.float16)[..., :s.states.shape[-1]]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("b,L,h,N,g,Q", F32_SHAPES)
+@pytest.mark.parametrize("with_dt,with_init", [(True, True), (False, False)])
+def test_chain_f16s_entry_point(b, L, h, N, g, Q, with_dt, with_init, dtype):
+    """16-bit inputs at chunk 64 / 128 with S_in handed over as "f16s" (f16
+    rows, a power-of-two scale per row): ssd_chunk_state_passing (the chain,
+    whose 4 waves per state row exchange the row maxima through LDS) against
+    chunk_state then state_passing(split="f16s"): the f16 values, the row
+    scales and the final state bit for bit."""
+    print("CASE chain f16s", dtype, b, L, h, N, g, Q, with_dt, with_init, flush=True)
+    X, A, B, C, dt, init = case(dtype, b, L, h, 64, N, g, seed=L + h + N + 1)
+    dt = dt if with_dt else None
+    init = init if with_init else None
+    Acs, decay = S.chunk_cumsum(A, Q)
+    S_in, final = S.chunk_state_passing(X, B, Acs, decay, dt=dt, initial_states=init, split="f16s")
+    st = S.chunk_state(X, B, Acs, dt=dt)
+    S_ref, f_ref = S.state_passing(st, decay, initial_states=init, split="f16s")
+    torch.cuda.synchronize()
+    assert torch.equal(final, f_ref)
+    assert torch.equal(S_in.scales, S_ref.scales)
+    assert torch.equal(_f16_halves(S_in), _f16_halves(S_ref))
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("b,L,h,N,g,Q", F32_SHAPES[:4])
+def test_16bit_forward_f16s_equals_kernels_one_by_one(b, L, h, N, g, Q, dtype):
+    """ssd_forward on 16-bit inputs at chunk 64 / 128 hands S_in to the 16-bit
+    chunk_scan as "f16s": Y and the final state bit for bit against K1, K2 + K3
+    (split="f16s") and K4 (split="f16s") through their own entry points."""
+    print("CASE 16-bit forward f16s", dtype, b, L, h, N, g, Q, flush=True)
+    X, A, B, C, dt, init = case(dtype, b, L, h, 64, N, g, seed=5 * L + h)
+    Y, final = S.ssd_forward(X, A, B, C, Q, dt=dt, initial_states=init, return_final_states=True)
+    Acs, decay = S.chunk_cumsum(A, Q)
+    S_in, fk = S.chunk_state_passing(X, B, Acs, decay, dt=dt, initial_states=init, split="f16s")
+    Yk = S.chunk_scan(X, B, C, Acs, S_in, dt=dt, split="f16s")
+    torch.cuda.synchronize()
+    assert torch.equal(final, fk)
+    assert torch.equal(Y, Yk)

@@ -109,6 +109,10 @@ struct WsLayout {
 
 // chunk_prep's outputs only exist for the persistent kernels' shapes
 bool prep_shape(const ssd_dims* d) { return d->chunk == 256 && (d->dstate == 64 || d->dstate == 128); }
+// The chunk-64 / 128 shapes whose 16-bit chunk_scan reads f16s states
+bool f16s_small_shape(const ssd_dims* d) {
+  return (d->chunk == 64 || d->chunk == 128) && (d->dstate == 64 || d->dstate == 128) && d->chunk * d->dstate <= 8192;
+}
 
 // prep buffer: the CB^T fragments, then (256-byte aligned) the B^T fragments
 size_t prep_cb_region(const ssd_dims* d) {
@@ -129,8 +133,10 @@ WsLayout ws_layout(const ssd_dims* d, int state_dtype) {
   w.decay = round_up(bhc * (size_t)d->chunk * sizeof(float));
   w.states = w.decay + round_up(bhc * sizeof(float));
   w.scales = w.states + round_up(bhc * (size_t)d->headdim * d->dstate * elem_size(state_dtype));
-  // the row scales of f16s-handed-over states (only with f32 states and the chunk-256 kernels' shapes)
-  const size_t scales = state_dtype == SSD_DTYPE_F32 && prep_shape(d) ? bhc * (size_t)d->headdim * sizeof(float) : 0;
+  // the row scales of f16s-handed-over states (only with f32 states, at the
+  // shapes where a 16-bit chunk_scan reads them)
+  const size_t scales =
+      state_dtype == SSD_DTYPE_F32 && (prep_shape(d) || f16s_small_shape(d)) ? bhc * (size_t)d->headdim * sizeof(float) : 0;
   w.prep = w.scales + round_up(scales);
   w.total = w.prep + prep_bytes(d);
   return w;
@@ -329,13 +335,20 @@ int run_state_passing(const ssd_dims* d, int dtype, const ChunkStateArgs& sa, co
 }
 
 // The format in which the forward hands f32 states from K3 to K4: 0 (plain
-// f32 or bf16 states), SSD_STATE_F16S or a SPLIT value; only the chunk-256
-// persistent chunk_scan reads the handover formats.
-int handover_format(const ssd_dims* d, int dtype, int state_dtype, const ChunkScanArgs& ca) {
+// f32 or bf16 states), SSD_STATE_F16S or a SPLIT value.  The chunk-256
+// persistent chunk_scan reads both handover formats; the 16-bit chunk_scan at
+// chunk 64 / 128 reads F16S (a SPLIT request there hands over plain f32).
+int handover_format(const ssd_dims* d, int dtype, int state_dtype, const ChunkScanArgs& ca, const float* scales) {
   if (!f32_layout(state_dtype) && state_dtype != SSD_DTYPE_F32) return 0;
-  if (!prep_applies(d, dtype) || !ssd::chunk_scan_persistent_supported(ca, dtype)) return 0;
-  if (state_dtype == SSD_DTYPE_F32 || state_dtype == SSD_STATE_F16S) return SSD_STATE_F16S;
-  return state_dtype;
+  const bool f16s = state_dtype == SSD_DTYPE_F32 || state_dtype == SSD_STATE_F16S;
+  if (prep_applies(d, dtype) && ssd::chunk_scan_persistent_supported(ca, dtype)) return f16s ? SSD_STATE_F16S : state_dtype;
+  if (f16s && f16s_small_shape(d)) {
+    ChunkScanArgs fa = ca;
+    fa.f16s = true;
+    fa.sscale = scales;
+    if (ssd::chunk_scan_b16_supported(fa, dtype, SSD_DTYPE_F32)) return SSD_STATE_F16S;
+  }
+  return 0;
 }
 
 int run_core(const ssd_dims* d, int dtype, const CumsumArgs* k1, const void* x, const int64_t x_strides[4],
@@ -366,15 +379,17 @@ int run_core(const ssd_dims* d, int dtype, const CumsumArgs* k1, const void* x, 
   } else if (k1) {
     if ((rc = hip_status(ssd::launch_chunk_cumsum(*k1, s)))) return rc;
   }
-  // f32 states for the chunk-256 chunk_scan: K3 (or the state chain) hands
-  // them over as f16 with per-row scales (the default), or as its hi/lo
-  // operand pairs when state_dtype asks for that format
+  // f32 states for a 16-bit chunk_scan that reads the handover formats: K3
+  // (or the state chain) hands them over as f16 with per-row scales (the
+  // default), or at chunk 256 as its hi/lo operand pairs when state_dtype
+  // asks for that format
   StatePassingArgs pa = make_sp_args(d, states, decay, initial_states, final_states);
-  const int handover = handover_format(d, dtype, state_dtype, ca);
+  float* scales = reinterpret_cast<float*>(ws + w.scales);
+  const int handover = handover_format(d, dtype, state_dtype, ca, scales);
   if (handover == SSD_STATE_F16S) {
     pa.f16s = 1;
     ca.f16s = true;
-    pa.sscale = reinterpret_cast<float*>(ws + w.scales);
+    pa.sscale = scales;
     ca.sscale = pa.sscale;
   } else if (handover) {
     pa.split_dtype = dtype;
@@ -679,11 +694,14 @@ int ssd_chunk_scan(const ssd_dims* d, int dtype, const void* x, const int64_t x_
   set_epilogue(p, epilogue);
   if (prep_applies(d, dtype)) p.cbf = prep_cbf(prep);
   if (split || f16s) {
-    // only the chunk-256 kernel reads the handover formats
-    if (!prep_applies(d, dtype) || !ssd::chunk_scan_persistent_supported(p, dtype)) return SSD_ERR_UNSUPPORTED_DTYPE;
+    // the chunk-256 kernel reads both handover formats, the 16-bit kernel at
+    // chunk 64 / 128 reads f16s
     p.presplit = split != 0;
     p.f16s = f16s;
     p.sscale = f16s ? state_scales : nullptr;
+    if (!(prep_applies(d, dtype) && ssd::chunk_scan_persistent_supported(p, dtype)) &&
+        !ssd::chunk_scan_b16_supported(p, dtype, SSD_DTYPE_F32))
+      return SSD_ERR_UNSUPPORTED_DTYPE;
   }
   return hip_status(ssd::launch_chunk_scan(p, dtype, f32_layout(state_dtype) ? SSD_DTYPE_F32 : state_dtype,
                                            (hipStream_t)stream));

@@ -255,9 +255,10 @@ hipError_t launch_t(const ChunkScanArgs& a, hipStream_t stream) {
 
 hipError_t launch_chunk_scan(const ChunkScanArgs& a, int dtype, int state_dtype, hipStream_t stream) {
   if (chunk_scan_persistent_supported(a, dtype)) return launch_chunk_scan_persistent(a, dtype, state_dtype, stream);
-  if (a.f16s || a.presplit) return hipErrorInvalidValue;  // formats of the persistent kernel only
-  if (chunk_scan_f32_supported(a, dtype, state_dtype)) return launch_chunk_scan_f32(a, stream);
+  // f16s: also the 16-bit kernel at chunk 64 / 128; the hi/lo pairs: the persistent kernel only
   if (chunk_scan_b16_supported(a, dtype, state_dtype)) return launch_chunk_scan_b16(a, dtype, stream);
+  if (a.f16s || a.presplit) return hipErrorInvalidValue;
+  if (chunk_scan_f32_supported(a, dtype, state_dtype)) return launch_chunk_scan_f32(a, stream);
   if (state_dtype == SSD_DTYPE_F32) {
     if (dtype == SSD_DTYPE_F32) return launch_t<float, float>(a, stream);
     if (dtype == SSD_DTYPE_BF16) return launch_t<bf16, float>(a, stream);

@@ -41,19 +41,25 @@ constexpr int kP = 64;
 constexpr int kNW = 8;
 constexpr int kThreads = 64 * kNW;
 
-template <typename T, int NK, int RT, bool HAS_DT>
+template <typename T, int NK, int RT, bool HAS_DT, bool F16S>
 __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs p, int hs, int slices) {
   constexpr int Q = 64 * RT;
   constexpr int N = 32 * NK;
-  constexpr int SPR = N / 4;                 // 16-byte pieces per f32 S_in row
+  // S_in rows as stored: N f32 values, or (F16S) the N f16 values in the
+  // first half of the row's f32 slots and a scale per row
+  constexpr int SRB = F16S ? N * 2 : N * 4;  // bytes per S_in row in LDS
+  constexpr int SPR = SRB / 16;              // 16-byte pieces per S_in row
   constexpr int XPW = Q * kP * 2 / 1024 / kNW;  // x copies (1 KB = 8 rows) per wave and head
-  constexpr int SPW = kP * N / 256 / kNW;       // S_in copies per wave and head
+  constexpr int SPW = kP * SRB / 1024 / kNW;    // S_in copies per wave and head
   constexpr int BPR = N * 2 / 16;            // 16-byte pieces per B row
   constexpr int BPW = Q * N * 2 / 1024 / kNW;   // B copies per wave (once per slice)
   constexpr int NSB = 2 * RT;                // 32-token s blocks of the chunk
   static_assert(XPW >= 1 && SPW >= 1 && BPW >= 1, "copies per wave");
+  // S_in's buffer also stages the chunk's B rows (Q N 2 bytes) once per slice
+  constexpr int SSB = kP * SRB > Q * N * 2 ? kP * SRB : Q * N * 2;
   __shared__ __attribute__((aligned(1024))) T xs[2][Q * kP];
-  __shared__ __attribute__((aligned(1024))) float ss[kP * N];
+  __shared__ __attribute__((aligned(1024))) float ss[SSB / 4];
+  __shared__ __attribute__((aligned(16))) float scl[F16S ? kP : 4];  // F16S: the row scales of S_in
   __shared__ __attribute__((aligned(16))) float al[2][Q];
   __shared__ __attribute__((aligned(16))) float dl[HAS_DT ? 2 : 1][HAS_DT ? Q : 4];
 
@@ -83,8 +89,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
 
   // ---- per-head copies: x, Acs, dt into buffer bf, S_in into its buffer ----
   // x rows s (64 elements, 8 pieces): copy block blk holds rows 8 blk ..
-  // 8 blk + 7, piece k of row s at slot k ^ (s & 7).  S_in rows r (N floats):
-  // piece k at slot k ^ (r & 7).
+  // 8 blk + 7, piece k of row s at slot k ^ (s & 7).
   const uint32_t xs_lds = lds_offset(&xs[0][0]), ss_lds = lds_offset(&ss[0]);
   const uint32_t al_lds = lds_offset(&al[0][0]), dl_lds = lds_offset(&dl[0][0]);
   const int64_t xcopy = (int64_t)(lane >> 3) * p.sxl + 8 * ((lane & 7) ^ (lane >> 3));
@@ -107,13 +112,26 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
       }
     }
   };
-  // S_in of head h into its (single) buffer
+  // S_in of head h into its (single) buffer: piece k of row r at slot
+  // k ^ ssw(r).  F16S: the 16 rows one operand read takes then lie on
+  // distinct banks (256-byte rows: r & 15; 128-byte rows, two per bank
+  // window: (r / 2) & 7); f32: r & 7
+  auto ssw = [](int r) __attribute__((always_inline)) {
+    if constexpr (!F16S) return r & 7;
+    else if constexpr (SPR >= 16) return r & 15;
+    else return (r >> 1) & 7;
+  };
+  const uint32_t scl_lds = lds_offset(&scl[0]);
   auto issue_sin = [&](int h) __attribute__((always_inline)) {
-    const float* sg = reinterpret_cast<const float*>(p.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (kP * N);
+    const int64_t item = ((int64_t)b * p.nchunks + c) * p.nheads + h;
+    const unsigned char* sg = reinterpret_cast<const unsigned char*>(reinterpret_cast<const float*>(p.states) + item * (kP * N));
 #pragma unroll
     for (int m = 0; m < SPW; ++m) {
-      const int blk = wave + kNW * m, r = blk * (64 / SPR) + lane / SPR, pc = (lane % SPR) ^ (r & 7);
-      dma16_at(sg + r * N + 4 * pc, ss_lds + (uint32_t)(blk * 1024));
+      const int blk = wave + kNW * m, r = blk * (64 / SPR) + lane / SPR, pc = (lane % SPR) ^ ssw(r);
+      dma16_at(sg + r * (N * 4) + 16 * pc, ss_lds + (uint32_t)(blk * 1024));
+    }
+    if constexpr (F16S) {
+      if (wave == 0) dma4_at(p.sscale + item * kP + lane, scl_lds);
     }
   };
   // f32 S_in -> MFMA operand pairs in place: each 32-byte pair
@@ -142,7 +160,6 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
   // B rows of the chunk (N elements of T, piece k of row s at slot k ^ (s %
   // BPR) so that the 16 rows one C.B^T operand read takes hit distinct banks)
   // into S_in's buffer, free until the first head's S_in is copied
-  // (Q N 2 <= kP N 4 bytes)
   const uint32_t bt_lds = ss_lds;
 #pragma unroll
   for (int m = 0; m < BPW; ++m) {
@@ -180,12 +197,49 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
         cbr[r][sb][st] = d;
       }
   }
+  // F16S: the off-diagonal product runs on f16 MFMAs, so each C row l of the
+  // wave's tiles is held as f16 scaled by a power of two 2^-e (its largest
+  // element then lies in [2^14, 2^15): bf16 values convert exactly), and
+  // cs[r] = 2^e undoes it with the decay factor of row l
+  float cs[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) cs[r] = 1.f;
+  if constexpr (F16S && !std::is_same<T, f16>::value) {
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      // largest |value| from the bf16 bit patterns (sign cleared, the order
+      // of non-negative bf16 values is that of their bits)
+      typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+      uint32_t mb = 0;
+#pragma unroll
+      for (int kc = 0; kc < NK; ++kc) {
+        const auto w = __builtin_bit_cast(u32x4, cf[r][kc]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) mb = max(mb, max(w[j] & 0x7fffu, (w[j] >> 16) & 0x7fffu));
+      }
+      float m = __uint_as_float(min(mb, 0x7f80u) << 16);  // a NaN counts as inf, as in every lane
+      // the row's 4 lane groups (lanes i, i + 16, i + 32, i + 48)
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
+      cs[r] = __builtin_ldexpf(1.f, e);
+#pragma unroll
+      for (int kc = 0; kc < NK; ++kc) {
+        f16x8 hv;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) hv[j] = (f16)__builtin_ldexpf(to_f32<T>(cf[r][kc][j]), -e);
+        cf[r][kc] = __builtin_bit_cast(frag8<T>, hv);
+      }
+    }
+  }
   __syncthreads();  // B's buffer takes the first head's S_in from here on
   issue_sin(h0);
   dma_wait();
   __syncthreads();
-  convert();
-  __syncthreads();
+  if constexpr (!F16S) {
+    convert();
+    __syncthreads();
+  }
 
   // x^T operand of p tile pt (via ds_read_b64_tr_b16): rows 4 g + i / 4
   // (+ 16, + 32 sb), columns 16 pt + 4 (i % 4), swizzled
@@ -220,7 +274,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
     if (h + 1 < h1) issue_head(h + 1, bf ^ 1);
     hprev = h;
     const T* xb = xs[bf];
-    const T* sb_ = reinterpret_cast<const T*>(&ss[0]);
+    const unsigned char* sb_ = reinterpret_cast<const unsigned char*>(&ss[0]);
     const float* ab = al[bf];
 
     // ---- off-diagonal: acc[p, l] = exp(Acs[l]) sum_n S_in[p, n] C[l, n] ----
@@ -232,18 +286,32 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
     for (int kc = 0; kc < NK; ++kc)
 #pragma unroll
       for (int e = 0; e < 2; ++e) {
-        // states 32 kc + 8 g .. + 7 of row p = 16 pt + i: pair q = 4 kc + g,
-        // hi at piece 2 q, lo at piece 2 q + 1 (swizzled by row & 7); 8 T per piece... in f32 slots
+        // states 32 kc + 8 g .. + 7 of row p = 16 pt + i (pair q = 4 kc + g):
+        // F16S, piece q of the f16 row; else the hi and lo of pair q at
+        // pieces 2 q and 2 q + 1
         const int row = 16 * (2 * ph + e) + i, q = 4 * kc + g;
-        const T* srow = sb_ + row * (2 * N);
-        const frag8<T> hi = *reinterpret_cast<const frag8<T>*>(srow + 8 * ((2 * q) ^ (row & 7)));
-        const frag8<T> lo = *reinterpret_cast<const frag8<T>*>(srow + 8 * ((2 * q + 1) ^ (row & 7)));
+        const unsigned char* srow = sb_ + row * SRB;
+        if constexpr (F16S) {
+          const f16x8 a = *reinterpret_cast<const f16x8*>(srow + 16 * (q ^ ssw(row)));
 #pragma unroll
-        for (int r = 0; r < RT; ++r) {
-          acc[r][e] = mma(hi, cf[r][kc], acc[r][e]);
-          acc[r][e] = mma(lo, cf[r][kc], acc[r][e]);
+          for (int r = 0; r < RT; ++r) acc[r][e] = mma(a, __builtin_bit_cast(f16x8, cf[r][kc]), acc[r][e]);
+        } else {
+          const frag8<T> hi = *reinterpret_cast<const frag8<T>*>(srow + 16 * ((2 * q) ^ ssw(row)));
+          const frag8<T> lo = *reinterpret_cast<const frag8<T>*>(srow + 16 * ((2 * q + 1) ^ ssw(row)));
+#pragma unroll
+          for (int r = 0; r < RT; ++r) {
+            acc[r][e] = mma(hi, cf[r][kc], acc[r][e]);
+            acc[r][e] = mma(lo, cf[r][kc], acc[r][e]);
+          }
         }
       }
+    // F16S: rows p carry their S_in row scale (4 consecutive p per lane),
+    // columns l the C row scale
+    f32x4 sc[2] = {f32x4{1.f, 1.f, 1.f, 1.f}, f32x4{1.f, 1.f, 1.f, 1.f}};
+    if constexpr (F16S) {
+#pragma unroll
+      for (int e = 0; e < 2; ++e) sc[e] = *reinterpret_cast<const f32x4*>(&scl[16 * (2 * ph + e) + 4 * g]);
+    }
     // every wave is done with S_in: the next head's comes in under the diagonal
     __syncthreads();
     if (h + 1 < h1) issue_sin(h + 1);
@@ -252,9 +320,9 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
       all[r] = ab[16 * trow[r] + i] * kLog2e;
-      const float e = __builtin_amdgcn_exp2f(all[r]);
+      const float e = __builtin_amdgcn_exp2f(all[r]) * cs[r];
 #pragma unroll
-      for (int ee = 0; ee < 2; ++ee) acc[r][ee] *= e;
+      for (int ee = 0; ee < 2; ++ee) acc[r][ee] *= F16S ? sc[ee] * e : f32x4{e, e, e, e};
     }
 
     // ---- diagonal: 32 tokens s per block; row tile t needs blocks sb <= t / 2 ----
@@ -301,7 +369,7 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
     }
     dma_wait();
     __syncthreads();
-    if (h + 1 < h1) {
+    if (!F16S && h + 1 < h1) {
       convert();
       __syncthreads();
     }
@@ -323,7 +391,8 @@ hipError_t launch_qn(const ChunkScanArgs& a, hipStream_t stream) {
   slices = (hpg + hs - 1) / hs;
   const int64_t grid = bcg * slices;
   if (grid > INT32_MAX) return hipErrorInvalidValue;
-  auto kern = a.dt ? chunk_scan_b16_kernel<T, NK, RT, true> : chunk_scan_b16_kernel<T, NK, RT, false>;
+  auto kern = a.f16s ? (a.dt ? chunk_scan_b16_kernel<T, NK, RT, true, true> : chunk_scan_b16_kernel<T, NK, RT, false, true>)
+                     : (a.dt ? chunk_scan_b16_kernel<T, NK, RT, true, false> : chunk_scan_b16_kernel<T, NK, RT, false, false>);
   kern<<<dim3((unsigned)grid), dim3(kThreads), 0, stream>>>(a, hs, slices);
   return hipGetLastError();
 }
@@ -340,7 +409,7 @@ hipError_t launch_t(const ChunkScanArgs& a, hipStream_t stream) {
 bool chunk_scan_b16_supported(const ChunkScanArgs& a, int dtype, int state_dtype) {
   return (dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16) && state_dtype == SSD_DTYPE_F32 &&
          (a.chunk == 64 || a.chunk == 128) && (a.dstate == 64 || a.dstate == 128) && a.chunk * a.dstate <= 8192 &&
-         !a.dskip && !a.z && !a.f16s && !a.presplit && !a.cbf;
+         !a.dskip && !a.z && !a.presplit && !a.cbf && (!a.f16s || a.sscale);
 }
 
 hipError_t launch_chunk_scan_b16(const ChunkScanArgs& a, int dtype, hipStream_t stream) {

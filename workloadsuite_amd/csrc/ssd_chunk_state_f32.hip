@@ -229,7 +229,12 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
 // states never reach memory.  x and B of the next chunk are copied
 // global -> LDS while the current chunk computes; the chains of one group's
 // heads run on one XCD and share B through its L2.
-template <typename T, int NK, int RT, bool HAS_DT, bool DB>
+// F16S (16-bit inputs, DB): S_in[c] goes out as SSD_STATE_F16S, f16 rows
+// with a power-of-two scale per row p, rounded exactly as state_passing's
+// f16s store rounds them; a row's N states lie in 4 waves, which exchange
+// their row maxima through LDS (written at the end of the previous chunk,
+// two buffers).
+template <typename T, int NK, int RT, bool HAS_DT, bool DB, bool F16S>
 __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkStateArgs p, StatePassingArgs sp) {
   constexpr int Q = 64 * RT;
   constexpr int N = 32 * NK;
@@ -243,6 +248,9 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
   __shared__ __attribute__((aligned(1024))) T bs[NBUF][Q * N];
   __shared__ __attribute__((aligned(16))) float al[NBUF][Q];
   __shared__ __attribute__((aligned(16))) float dl[HAS_DT ? NBUF : 1][HAS_DT ? Q : 4];
+  static_assert(!F16S || DB, "the f16s store needs the double-buffered loop");
+  // F16S: the largest |S_in| of row p over n quarter k (waves 2 k, 2 k + 1)
+  __shared__ float rmax[F16S ? 2 : 1][F16S ? 4 * kP : 1];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -287,6 +295,22 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
 #pragma unroll
     for (int n = 0; n < NTW; ++n)
       st[a][n] = sp.init ? *reinterpret_cast<const f32x4*>(sp.init + bh * PN + sidx(a, n)) : f32x4{0.f, 0.f, 0.f, 0.f};
+  // F16S: this wave's part of the row maxima of the running state (lanes
+  // i, i + 16, i + 32, i + 48 hold row p's 16 n of each of its n tiles)
+  auto put_rmax = [&](int buf) __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < 2; ++a) {
+      float m = 0.f;
+#pragma unroll
+      for (int n = 0; n < NTW; ++n)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) m = fmaxf(m, fabsf(st[a][n][k]));
+      m = fmaxf(m, __shfl_xor(m, 16));
+      m = fmaxf(m, __shfl_xor(m, 32));
+      if (g == 0) rmax[buf][(wave >> 1) * kP + 16 * (2 * pp + a) + i] = m;
+    }
+  };
+  if constexpr (F16S) put_rmax(0);
   if constexpr (DB) {
     issue_chunk(0, 0);
     dma_wait();
@@ -313,10 +337,31 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
     } else {
       issue_chunk(c, 0);
     }
+    if constexpr (F16S) {
+      // row p's f16 values in the first half of its f32 slots, its scale in
+      // sscale[b, c, h, p] (written by the lanes of n quarter 0)
+      const float* rm = rmax[c & 1];
 #pragma unroll
-    for (int a = 0; a < 2; ++a)
+      for (int a = 0; a < 2; ++a) {
+        const int pr = 16 * (2 * pp + a) + i;
+        const float m = fmaxf(fmaxf(rm[pr], rm[kP + pr]), fmaxf(rm[2 * kP + pr], rm[3 * kP + pr]));
+        const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
 #pragma unroll
-      for (int n = 0; n < NTW; ++n) *reinterpret_cast<f32x4*>(sg + sidx(a, n)) = st[a][n];
+        for (int n = 0; n < NTW; ++n) {
+          f16x4 hv;
+#pragma unroll
+          for (int k = 0; k < 4; ++k) hv[k] = (f16)__builtin_ldexpf(st[a][n][k], -e);
+          *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(sg + pr * N) + 16 * (nt0 + n) + 4 * g) = hv;
+        }
+        if (nt0 == 0 && g == 0)
+          sp.sscale[(((int64_t)b * p.nchunks + c) * p.nheads + h) * kP + pr] = __builtin_ldexpf(1.f, e);
+      }
+    } else {
+#pragma unroll
+      for (int a = 0; a < 2; ++a)
+#pragma unroll
+        for (int n = 0; n < NTW; ++n) *reinterpret_cast<f32x4*>(sg + sidx(a, n)) = st[a][n];
+    }
     if constexpr (!DB) {
       vm_wait<kStores>();
       __syncthreads();
@@ -363,6 +408,7 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
     for (int a = 0; a < 2; ++a)
 #pragma unroll
       for (int n = 0; n < NTW; ++n) st[a][n] = st[a][n] * dec + acc[a][n];
+    if constexpr (F16S) put_rmax((c + 1) & 1);
     // DB: the next chunk's copies have landed (the stores may still be in
     // flight); either way every wave is done with this chunk's buffer
     if constexpr (DB) vm_wait<kStores>();
@@ -389,8 +435,15 @@ hipError_t launch_chain_qn(const ChunkStateArgs& a, const StatePassingArgs& sp, 
   // chains of 32 chunks: 404 -> 378 us)
   const int cus = device_cu_count() > 0 ? device_cu_count() : 256;
   const bool db = chains < 2 * (int64_t)cus || !std::is_same<T, float>::value;
-  auto kern = db ? (a.dt ? chunk_state_chain_f32_kernel<T, NK, RT, true, true> : chunk_state_chain_f32_kernel<T, NK, RT, false, true>)
-                 : (a.dt ? chunk_state_chain_f32_kernel<T, NK, RT, true, false> : chunk_state_chain_f32_kernel<T, NK, RT, false, false>);
+  if constexpr (!std::is_same<T, float>::value) {
+    if (sp.f16s) {
+      auto kern = a.dt ? chunk_state_chain_f32_kernel<T, NK, RT, true, true, true> : chunk_state_chain_f32_kernel<T, NK, RT, false, true, true>;
+      kern<<<dim3((unsigned)chains), dim3(kThreads), 0, stream>>>(a, sp);
+      return hipGetLastError();
+    }
+  }
+  auto kern = db ? (a.dt ? chunk_state_chain_f32_kernel<T, NK, RT, true, true, false> : chunk_state_chain_f32_kernel<T, NK, RT, false, true, false>)
+                 : (a.dt ? chunk_state_chain_f32_kernel<T, NK, RT, true, false, false> : chunk_state_chain_f32_kernel<T, NK, RT, false, false, false>);
   kern<<<dim3((unsigned)chains), dim3(kThreads), 0, stream>>>(a, sp);
   return hipGetLastError();
 }
@@ -435,9 +488,11 @@ bool chunk_state_f32_supported(const ChunkStateArgs& a, int dtype, int state_dty
 }
 
 bool chunk_state_chain_f32_supported(const ChunkStateArgs& a, int dtype, const StatePassingArgs& sp) {
-  // two chunks of x and B in LDS: chunk x d_state up to 8192
+  // two chunks of x and B in LDS: chunk x d_state up to 8192; S_in as f16s
+  // for 16-bit inputs
   return chunk_state_f32_supported(a, dtype, SSD_DTYPE_F32) && a.chunk * a.dstate <= 8192 && !sp.split_dtype &&
-         !sp.f16s && sp.bh_begin == 0 && (sp.bh_count == 0 || sp.bh_count == a.batch * a.nheads);
+         (!sp.f16s || (dtype != SSD_DTYPE_F32 && sp.sscale)) && sp.bh_begin == 0 &&
+         (sp.bh_count == 0 || sp.bh_count == a.batch * a.nheads);
 }
 
 hipError_t launch_chunk_state_chain_f32(const ChunkStateArgs& a, const StatePassingArgs& sp, int dtype, hipStream_t stream) {
