@@ -96,12 +96,35 @@ def kernel_model(cfg, state_dtype, handover=None, local_f16=False):
     }
 
 
-def takes_state_chain(cfg, split):
-    """ssd_forward's dispatch for K2 + K3 at chunk 256 with a hand-over format
-    (chunk_state_chain_plan in the library): one state-chain launch when the
+def small_chunk_shape(cfg):
+    """chunk 64 / 128, d_state 64 / 128, chunk x d_state <= 8192: the shapes of
+    the f32-state chain and of the 16-bit chunk_scan for f32 states."""
+    return cfg.chunk in (64, 128) and cfg.dstate in (64, 128) and cfg.chunk * cfg.dstate <= 8192
+
+
+def handover_format(cfg, state_dtype, prep, state_format):
+    """The format ssd_forward hands f32 S_in to K4 in (handover_format in the
+    library): at chunk 256 with 16-bit inputs "f16s", or the inputs' (hi, lo)
+    pairs with --state-format split; at the small-chunk shapes with 16-bit
+    inputs "f16s" (a split request hands over plain f32 there); else None."""
+    if state_dtype != torch.float32 or cfg.dtype == torch.float32:
+        return None
+    if prep is not None:
+        return cfg.dtype if state_format == "split" else "f16s"
+    if small_chunk_shape(cfg) and state_format != "split":
+        return "f16s"
+    return None
+
+
+def takes_state_chain(cfg, split, state_dtype):
+    """ssd_forward's dispatch for K2 + K3: at chunk 64 / 128 the f32-state
+    chain wherever its shape allows; at chunk 256 with a hand-over format
+    (chunk_state_chain_plan in the library) one state-chain launch when the
     (batch, head) chains keep every CU about equally busy (at least 3/4 of the
     busiest CU's chains on the average CU) or number between one and two per
     CU (d_state 128 for "f16s"); otherwise chunk_state then state_passing."""
+    if cfg.chunk != 256:
+        return state_dtype == torch.float32 and small_chunk_shape(cfg)
     if split is None or (split == "f16s" and cfg.dstate != 128):
         return False
     chains = cfg.batch * cfg.nheads
@@ -282,7 +305,7 @@ def main():
     ap.add_argument("--config", default=HEADLINE, choices=sorted(CONFIGS))
     ap.add_argument("--state-dtype", default="f32", choices=["f32", "bf16"])
     ap.add_argument("--state-format", default=None, choices=["split", "f16s"],
-                    help="how f32 states reach chunk_scan (default: the library's choice, f16s at chunk 256)")
+                    help="how f32 states reach chunk_scan (default: the library's choice, f16s for 16-bit inputs)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-reps", type=int, default=30)
     ap.add_argument("--layer", action="store_true",
@@ -345,15 +368,14 @@ def main():
     Acs, decay = S.chunk_cumsum(A, cfg.chunk)
     prep = S.chunk_prep(B, C, cfg.chunk)
     states = S.chunk_state(X, B, Acs, state_dtype=state_dtype, prep=prep)
-    # as in ssd_forward: with prep (chunk 256, 16-bit inputs) and f32 states, K3
-    # hands S_in to K4 as f16 rows with a power-of-two scale per row ("f16s"),
-    # or as 16-bit (hi, lo) pairs with --state-format split
-    split = None
-    if prep is not None and state_dtype == torch.float32:
-        split = cfg.dtype if args.state_format == "split" else "f16s"
+    # as in ssd_forward: with 16-bit inputs and f32 states, K3 hands S_in to K4
+    # as f16 rows with a power-of-two scale per row ("f16s"), or at chunk 256
+    # as 16-bit (hi, lo) pairs with --state-format split
+    split = handover_format(cfg, state_dtype, prep, args.state_format)
     # where the forward runs chunk_state then state_passing with the f16s
-    # hand-over, the local states cross HBM as f16 rows: time those variants
-    local_f16 = split == "f16s" and not takes_state_chain(cfg, split)
+    # hand-over at chunk 256, the local states cross HBM as f16 rows: time
+    # those variants
+    local_f16 = split == "f16s" and prep is not None and not takes_state_chain(cfg, split, state_dtype)
     if local_f16:
         states = S.chunk_state(X, B, Acs, state_dtype="f16s", prep=prep).states
     S_in, _ = S.state_passing(S.F16SLocalStates(states) if local_f16 else states, decay, init, split=split)
@@ -439,7 +461,8 @@ def main():
                    "inputs": f"{DTYPE_NAMES[cfg.dtype]} X/B/C, f32 A", "state_storage": args.state_dtype,
                    "state_handover": split if isinstance(split, str) else ("split" if split is not None else None),
                    "local_states": ("f16 rows" if local_f16 else
-                                    "in registers (state chain)" if takes_state_chain(cfg, split) else args.state_dtype),
+                                    "in registers (state chain)" if takes_state_chain(cfg, split, state_dtype)
+                                    else args.state_dtype),
                    "final_state": cfg.final_state, "initial_state": cfg.init_state},
         "device_ms_per_step": round(dev_ms, 5),
         "step_stats": stats,

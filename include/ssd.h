@@ -63,10 +63,13 @@ extern "C" {
  * ssd_state_passing and ssd_chunk_state_passing write SPLIT and F16S from f32
  * (or F16S_LOCAL) local states; ssd_chunk_scan reads them, for 16-bit inputs
  * at chunk 256 and dstate 64 / 128 (F16S with dstate 128 for the one-launch
- * state chain), as MFMA operands without converting them.  ssd_chunk_state
- * writes F16S_LOCAL for 16-bit inputs at chunk 256 and dstate 64 / 128.
- * ssd_forward hands the states to chunk_scan as F16S wherever that applies
- * (state_dtype SSD_DTYPE_F32), or in the format state_dtype names. */
+ * state chain), as MFMA operands without converting them, and reads F16S for
+ * 16-bit inputs at chunk 64 / 128, dstate 64 / 128, chunk x dstate <= 8192,
+ * without the epilogue.  ssd_chunk_state writes F16S_LOCAL for 16-bit inputs
+ * at chunk 256 and dstate 64 / 128.  ssd_forward hands the states to
+ * chunk_scan as F16S wherever that applies (state_dtype SSD_DTYPE_F32), or in
+ * the format state_dtype names (at chunk 256; a SPLIT state_dtype at chunk
+ * 64 / 128 hands over plain f32). */
 enum {
   SSD_DTYPE_F32 = 0,
   SSD_DTYPE_BF16 = 1,
@@ -117,9 +120,11 @@ const char* ssd_strerror(int status);
 int ssd_check_dims(const ssd_dims* d, int dtype);
 
 /* Bytes of workspace ssd_forward needs: a_cumsum, chunk_decay, the
- * per-chunk states (state_dtype: SSD_DTYPE_F32 or SSD_DTYPE_BF16) and
- * ssd_chunk_prep_bytes(d), each region 256-byte aligned.  0 when dims are
- * invalid. */
+ * per-chunk states (state_dtype: SSD_DTYPE_F32 or SSD_DTYPE_BF16), for f32
+ * states at the shapes where a 16-bit chunk_scan reads F16S (chunk 256, or
+ * chunk 64 / 128 with chunk x dstate <= 8192; dstate 64 / 128) their row
+ * scales [b, c, h, P] f32, and ssd_chunk_prep_bytes(d), each region 256-byte
+ * aligned.  0 when dims are invalid. */
 size_t ssd_workspace_bytes(const ssd_dims* d, int state_dtype);
 
 /* K1 -- intra-chunk cumsum of the log-decays and the per-chunk total decay.
@@ -179,8 +184,8 @@ int ssd_state_passing(const ssd_dims* d, void* states, int state_dtype, float* s
  * ssd_chunk_state (f32 local states for the SPLIT formats and F16S, else
  * state_dtype) followed by ssd_state_passing would leave it.  For a SPLIT
  * state_dtype of the inputs' type or F16S with prep (chunk 256), and for f32
- * inputs with f32 states at chunk 64 / 128 and dstate 64 / 128 (chunk x
- * dstate <= 8192), the two stages run as one launch (for SPLIT and F16S,
+ * states (or F16S with 16-bit inputs) at chunk 64 / 128 and dstate 64 / 128
+ * (chunk x dstate <= 8192), the two stages run as one launch (at chunk 256,
  * wherever that is faster on the device): each (b, h) chain of chunks keeps
  * its running state in registers and the local states are never stored.
  * Where F16S's two stages run as separate launches (16-bit inputs at chunk

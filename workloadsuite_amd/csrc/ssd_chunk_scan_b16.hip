@@ -1,5 +1,7 @@
-// K4 -- chunk_scan for 16-bit inputs with f32 states at chunk 64 / 128 and
-// d_state 64 / 128 (MR's own block_len 64 at the production layer shape).
+// K4 -- chunk_scan for 16-bit inputs with f32 states (plain f32, or the
+// SSD_STATE_F16S hand-over: f16 rows with a power-of-two scale per row) at
+// chunk 64 / 128 and d_state 64 / 128 (MR's own block_len 64 at the
+// production layer shape).
 // Same result as the generic kernel in ssd_chunk_scan.hip up to rounding
 // (workloads/mamba/model_ref.py:139-145, 160-162):
 //   y[l, p] = sum_{s<=l} exp(Acs[l]-Acs[s]) (C_l . B_s) dt[s] x[s, p]
@@ -23,7 +25,10 @@
 //     registers, kept as f32 D fragments (4 consecutive s per lane);
 //   * the off-diagonal S_in . C^T: each head's f32 S_in is split in LDS, once,
 //     into a hi + lo pair of the input type (~16 significant bits through the
-//     MFMA: hi = round(v), lo = round(v - hi)), two MFMAs per K step;
+//     MFMA: hi = round(v), lo = round(v - hi)), two MFMAs per K step; f16s
+//     S_in is read as it lies (half the bytes) on one f16 MFMA per K step,
+//     with the C rows held as f16 times a power of two per row and both
+//     scales applied to the f32 result;
 //   * the diagonal x^T . (decay . C.B^T): x^T straight from row-major x in LDS
 //     through ds_read_b64_tr_b16 (rows XOR-swizzled by 16-byte piece at copy
 //     time), the weighted C.B^T block rounded to the input type once.

@@ -201,15 +201,16 @@ bool chunk_scan_f32_supported(const ChunkScanArgs& a, int dtype, int state_dtype
 bool chunk_state_f32_supported(const ChunkStateArgs& a, int dtype, int state_dtype);
 hipError_t launch_chunk_state_f32(const ChunkStateArgs& a, int dtype, hipStream_t stream);
 // ... and K2 + K3 as one launch for f32 states (one workgroup per (b, h)
-// chain, S_in written in place of the local states in the f32 layout):
-// bit-identical to launch_chunk_state_f32 followed by launch_state_passing.
+// chain, S_in written in place of the local states in the f32 layout, or for
+// 16-bit inputs as f16s with sp.sscale): bit-identical to
+// launch_chunk_state_f32 followed by launch_state_passing.
 bool chunk_state_chain_f32_supported(const ChunkStateArgs& a, int dtype, const StatePassingArgs& sp);
 hipError_t launch_chunk_state_chain_f32(const ChunkStateArgs& a, const StatePassingArgs& sp, int dtype, hipStream_t stream);
 hipError_t launch_chunk_scan_f32(const ChunkScanArgs& a, hipStream_t stream);
-// chunk_scan for 16-bit inputs with f32 states at chunk 64 / 128, d_state
-// 64 / 128, without the layer epilogue (ssd_chunk_scan_b16.hip): the f32
-// kernel's decomposition on 16-bit MFMAs; launch_chunk_scan dispatches to it
-// when supported.
+// chunk_scan for 16-bit inputs with f32 states (plain, or f16s with
+// a.sscale) at chunk 64 / 128, d_state 64 / 128, without the layer epilogue
+// (ssd_chunk_scan_b16.hip): the f32 kernel's decomposition on 16-bit MFMAs;
+// launch_chunk_scan dispatches to it when supported.
 bool chunk_scan_b16_supported(const ChunkScanArgs& a, int dtype, int state_dtype);
 hipError_t launch_chunk_scan_b16(const ChunkScanArgs& a, int dtype, hipStream_t stream);
 
