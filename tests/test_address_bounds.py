@@ -411,9 +411,15 @@ def test_f32_kernel_addresses(name):
         "const int row = 32 * sb + 16 * st + i, pc = 8 * kc + 2 * g;",
         "bf8.hi = *reinterpret_cast<const f32x4*>(brow + 4 * ((pc + 1) ^ (row & 7)));")
     pin("ssd_chunk_state_f32.hip",
-        "return (sizeof(T) == 4 ? 4 : 2) * ((l >> 2) & 3);",
-        "return l * cols + EPP * ((col / EPP) ^ swz_x<T>(l)) + col % EPP;",
-        "const int ppr = cols * (int)sizeof(T) / 16, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ swz_x<T>(r);",
+        "if constexpr (sizeof(T) == 4) return 4 * ((l >> 2) & 3);",
+        "else return cols * 2 >= 256 ? 2 * (l & 7) : 2 * ((l >> 1) & 3);",
+        "return l * cols + EPP * ((col / EPP) ^ swz_x<T>(l, cols)) + col % EPP;",
+        "const int ppr = cols * (int)sizeof(T) / 16, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ swz_x<T>(r, cols);",
+        "const int r = 32 * ks + 4 * g + (i >> 2), c = c0 + 4 * (i & 3);",
+        "return join<T>(lds_read_tr(blk + swz_off<T>(r, c, cols)), lds_read_tr(blk + swz_off<T>(r + 16, c, cols)));",
+        "bfr[n][ks] = tr_operand<T>(bl, ks, 16 * (nt0 + n), N, g, i);",
+        "bfr[n] = tr_operand<T>(bl, ks, 16 * (nt0 + n), N, g, i);",
+        "xr = tr_operand<T>(xb, ks, 16 * (2 * pp + a), kP, g, i);",
         "dma16_at(src + r * ld + (16 / (int)sizeof(T)) * pc, dst + (uint32_t)(blk * 1024));",
         "constexpr int XPW = Q * kP * ES / 1024 / kNW;",
         "constexpr int BPW = Q * N * ES / 1024 / kNW;",
@@ -466,12 +472,18 @@ def test_f32_kernel_addresses(name):
     inside("chunk_scan B fragment floats", 4 * (bpc[..., None] ^ np.arange(8)) + 3, 0, N)
     # x and B copies of chunk_state and the chain (stage_rows), for f32 and
     # 16-bit inputs: rows of `cols` elements in 16-byte pieces, piece k of row
-    # r from piece k ^ swz_x(r); operand reads at swz_off
+    # r from piece k ^ swz_x(r); operand reads at swz_off (f32: element-wise;
+    # 16-bit: the transposing reads' 4-element runs, below)
     for es in (4, 2):
         epp = 16 // es
-        swx = lambda r: (4 if es == 4 else 2) * ((r >> 2) & 3)  # noqa: E731
         lds_e = max(2 * Q * P, Q * P + Q * N)
         for cols, name in ((P, "x"), (N, "B")):
+            if es == 4:
+                swx = lambda r: 4 * ((r >> 2) & 3)  # noqa: E731
+            elif cols * 2 >= 256:
+                swx = lambda r: 2 * (r & 7)  # noqa: E731
+            else:
+                swx = lambda r: 2 * ((r >> 1) & 3)  # noqa: E731
             ppr = cols * es // 16
             ncp = Q * cols * es // 1024
             assert ncp % 8 == 0, (name, es)
@@ -486,6 +498,27 @@ def test_f32_kernel_addresses(name):
             col = np.arange(cols)[:, None, None, None, None]
             off = l_ * cols + epp * ((col // epp) ^ swx(l_)) + col % epp
             inside(f"{name} operand reads ({es}-byte)", off, 0, Q * cols)
+            inside(f"{name} piece swizzle ({es}-byte)", swx(np.arange(Q)), 0, ppr)
+            if es == 2:
+                # transposing reads: rows 32 ks + 4 g + i / 4 (+ 16), 4 elements
+                # from column c0 + 4 (i % 4), c0 = 16 t for the operand's column tile
+                ks_ = np.arange(Q // 32)[:, None, None, None]
+                t_ = np.arange(cols // 16)[:, None, None]
+                r_ = 32 * ks_ + 4 * g + (i >> 2)
+                c_ = 16 * t_ + 4 * (i & 3)
+                for rr in (r_, r_ + 16):
+                    inside(f"{name} tr rows", rr, 0, Q)
+                    o = rr * cols + epp * ((c_ // epp) ^ swx(rr)) + c_ % epp
+                    inside(f"{name} tr elements", o + 3, 0, Q * cols)
+                    assert ((c_ % epp) + 3 < epp).all()     # 4 elements within one piece
+                # 8 consecutive rows' 32-byte segments (lanes 0-31 or 32-63 of
+                # one read) on distinct 8-byte bank slots of a 256-byte window
+                for t in range(cols // 16):
+                    for r0 in range(0, Q, 8):
+                        rows = np.arange(r0, r0 + 8)[:, None]
+                        cc = 16 * t + 4 * np.arange(4)[None, :]
+                        byte = 2 * (rows * cols + epp * ((cc // epp) ^ swx(rows)) + cc % epp)
+                        assert len(set((byte % 256 // 8).ravel().tolist())) == 32, (name, t, r0)
     # Acs and dt copies
     inside("Acs (lanes < Q / 4)", 4 * np.arange(Q // 4) + 3, 0, Q)
     part = np.arange(Q // 64)[:, None]

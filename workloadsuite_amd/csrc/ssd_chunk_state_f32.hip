@@ -37,24 +37,42 @@ constexpr int kNW = 8;
 constexpr int kThreads = 64 * kNW;
 
 // Staged rows of x and B: 16-byte pieces of EPP = 16 / sizeof(T) elements,
-// piece k of row l stored at piece k ^ swz_x(l).  A fragment read takes one
-// column of rows 4 g + jj (g = 0..3): the XOR moves those 4 rows to 4
-// different 64-byte (f32) or 32-byte (16-bit) bank groups.
-template <typename T> __device__ __forceinline__ int swz_x(int l) {
-  return (sizeof(T) == 4 ? 4 : 2) * ((l >> 2) & 3);
+// piece k of row l stored at piece k ^ swz_x(l).  f32: a fragment read takes
+// one column of rows 4 g + jj (g = 0..3), and the XOR moves those 4 rows to 4
+// different 64-byte bank groups.  16-bit: the operands come through
+// transposing reads (tr_operand), in which 32 lanes take 32 bytes (a pair of
+// pieces) of each of 8 consecutive rows; the XOR (a multiple of 2, so pairs
+// stay whole) puts those 8 row segments on distinct banks (rows of >= 256
+// bytes: 2 (l & 7); rows of 128 bytes, two per 256-byte bank window: the
+// window half l & 1 and 2 ((l / 2) & 3)).
+template <typename T> __device__ __forceinline__ int swz_x(int l, int cols) {
+  if constexpr (sizeof(T) == 4) return 4 * ((l >> 2) & 3);
+  else return cols * 2 >= 256 ? 2 * (l & 7) : 2 * ((l >> 1) & 3);
 }
 // element offset of x / B element (l, col) in a staged block of rows of `cols` elements
 template <typename T> __device__ __forceinline__ int swz_off(int l, int col, int cols) {
   constexpr int EPP = 16 / (int)sizeof(T);
-  return l * cols + EPP * ((col / EPP) ^ swz_x<T>(l)) + col % EPP;
+  return l * cols + EPP * ((col / EPP) ^ swz_x<T>(l, cols)) + col % EPP;
 }
 // global -> LDS copy blk (1 KB, 64 lanes x 16 bytes) of rows of `cols`
 // elements of T, rows ld elements apart, into dst + 1 KB blk (piece k of row
 // r from piece k ^ swz_x(r) of the global row)
 template <typename T>
 __device__ __forceinline__ void stage_rows(const T* src, int64_t ld, int cols, int blk, uint32_t dst, int lane) {
-  const int ppr = cols * (int)sizeof(T) / 16, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ swz_x<T>(r);
+  const int ppr = cols * (int)sizeof(T) / 16, r = blk * (64 / ppr) + lane / ppr, pc = (lane % ppr) ^ swz_x<T>(r, cols);
   dma16_at(src + r * ld + (16 / (int)sizeof(T)) * pc, dst + (uint32_t)(blk * 1024));
+}
+// 16-bit inputs: the MFMA operand of K step ks for column c0 + i (c0 a
+// multiple of 16) from a staged block of rows of `cols` elements, as two
+// transposing reads: lane (i, g) addresses row 32 ks + 4 g + i / 4 (then 16
+// rows on), columns c0 + 4 (i % 4) .. + 3, and receives column c0 + i of
+// rows 4 g .. 4 g + 3 -- K slot j holds token 32 ks + 16 (j / 4) + 4 g + j % 4,
+// the slot order of the element-wise reads (ds_read_b64_tr_b16, as chunk_scan
+// reads x^T)
+template <typename T>
+__device__ __forceinline__ frag8<T> tr_operand(const T* blk, int ks, int c0, int cols, int g, int i) {
+  const int r = 32 * ks + 4 * g + (i >> 2), c = c0 + 4 * (i & 3);
+  return join<T>(lds_read_tr(blk + swz_off<T>(r, c, cols)), lds_read_tr(blk + swz_off<T>(r + 16, c, cols)));
 }
 
 // w[l] = exp(Acs[Q-1] - Acs[l]) dt[l] from Acs[l], log2(e) Acs[Q-1] and dt[l]
@@ -153,10 +171,15 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
 #pragma unroll
     for (int n = 0; n < NTW; ++n)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
+      for (int ks = 0; ks < KS; ++ks) {
+        if constexpr (std::is_same<T, float>::value) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          bfr[n][ks][j] = bl[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)];
+          for (int j = 0; j < 8; ++j)
+            bfr[n][ks][j] = bl[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)];
+        } else {
+          bfr[n][ks] = tr_operand<T>(bl, ks, 16 * (nt0 + n), N, g, i);
+        }
+      }
   }
   __syncthreads();  // B's LDS is x buffer 1 from here on
 
@@ -203,10 +226,14 @@ __global__ __launch_bounds__(kThreads) void chunk_state_f32_kernel(ChunkStateArg
       }
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
-        const int col = 16 * (2 * pp + a) + i;
         frag8<T> xr;
+        if constexpr (std::is_same<T, float>::value) {
+          const int col = 16 * (2 * pp + a) + i;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xr[j] = xb[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)];
+          for (int j = 0; j < 8; ++j) xr[j] = xb[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)];
+        } else {
+          xr = tr_operand<T>(xb, ks, 16 * (2 * pp + a), kP, g, i);
+        }
 #pragma unroll
         for (int n = 0; n < NTW; ++n) acc[a][n] = kstep<T>(bfr[n][ks], xr, w, acc[a][n]);
       }
@@ -251,6 +278,9 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
   static_assert(!F16S || DB, "the f16s store needs the double-buffered loop");
   // F16S: the largest |S_in| of row p over n quarter k (waves 2 k, 2 k + 1)
   __shared__ float rmax[F16S ? 2 : 1][F16S ? 4 * kP : 1];
+  // each wave's copy of the current chunk's weights w[l] (written and read by
+  // that wave only)
+  __shared__ __attribute__((aligned(16))) float wl[kNW][Q];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -370,6 +400,14 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
     const T* bl = bs[bf];
     const float* ab = al[bf];
     const float last = ab[Q - 1] * kLog2e;
+    // the chunk's weights, token 64 k + lane by each lane, into this wave's
+    // copy (the same values as forming each lane's 8 weights per K step)
+    float* wv = wl[wave];
+#pragma unroll
+    for (int k = 0; k < Q / 64; ++k) {
+      const int l = 64 * k + lane;
+      wv[l] = chunk_weight(ab[l], last, HAS_DT ? dl[bf][l] : 1.f);
+    }
     f32x4 acc[2][NTW];
 #pragma unroll
     for (int a = 0; a < 2; ++a)
@@ -380,25 +418,31 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
       float w[8];
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const int l = 32 * ks + 16 * s2 + 4 * g;
-        const f32x4 a4 = *reinterpret_cast<const f32x4*>(ab + l);
-        f32x4 d4 = f32x4{1.f, 1.f, 1.f, 1.f};
-        if constexpr (HAS_DT) d4 = *reinterpret_cast<const f32x4*>(&dl[bf][l]);
+        const f32x4 w4 = *reinterpret_cast<const f32x4*>(wv + 32 * ks + 16 * s2 + 4 * g);
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) w[4 * s2 + jj] = chunk_weight(a4[jj], last, d4[jj]);
+        for (int jj = 0; jj < 4; ++jj) w[4 * s2 + jj] = w4[jj];
       }
       BFrag<T> bfr[NTW];
 #pragma unroll
-      for (int n = 0; n < NTW; ++n)
+      for (int n = 0; n < NTW; ++n) {
+        if constexpr (std::is_same<T, float>::value) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          bfr[n][j] = bl[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)];
+          for (int j = 0; j < 8; ++j)
+            bfr[n][j] = bl[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), 16 * (nt0 + n) + i, N)];
+        } else {
+          bfr[n] = tr_operand<T>(bl, ks, 16 * (nt0 + n), N, g, i);
+        }
+      }
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
-        const int col = 16 * (2 * pp + a) + i;
         frag8<T> xr;
+        if constexpr (std::is_same<T, float>::value) {
+          const int col = 16 * (2 * pp + a) + i;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xr[j] = xb[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)];
+          for (int j = 0; j < 8; ++j) xr[j] = xb[swz_off<T>(32 * ks + 16 * (j >> 2) + 4 * g + (j & 3), col, kP)];
+        } else {
+          xr = tr_operand<T>(xb, ks, 16 * (2 * pp + a), kP, g, i);
+        }
 #pragma unroll
         for (int n = 0; n < NTW; ++n) acc[a][n] = kstep<T>(bfr[n], xr, w, acc[a][n]);
       }
