@@ -91,6 +91,26 @@ def test_k2_chunk_state(dtype, Q, N):
     assert_close(states, S_ref, tolerance(dtype))
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("Q,N", [(64, 128), (64, 64), (128, 64), (128, 128)])
+def test_k2_16bit_inputs_keep_f32_accuracy(dtype, Q, N):
+    """chunk_state with 16-bit inputs and f32 states at chunk 64 / 128: the
+    weighted x goes through the MFMA as a hi + lo pair of the input type, so
+    the states match the float64 oracle on the same (exactly converted)
+    inputs to f32 accumulation accuracy.  Tolerance 3e-5 of max|S| (64-128
+    f32 products per element); with hi alone the error is ~2e-4 of max|S|.
+    With dt, chunk 64 / 128 x d_state 64 / 128 (the 4-n-tile and 8-n-tile
+    operand reads), 3 chunks of 5 heads in 1 group."""
+    say("k2 16-bit accuracy", dtype, Q, N)
+    cfg, inp = small_case(dtype, Q, N, b=1, nc=3, h=5, g=1)
+    dt = torch.rand(1, 3 * Q, 5, generator=torch.Generator().manual_seed(7)) + 0.5
+    rAcs, _ = O.chunk_cumsum(inp["A"].double(), Q)
+    S_ref = O.chunk_state(inp["X"].double(), inp["B"].double(), rAcs, dt=dt.double())
+    d = to_dev(inp)
+    states = S.chunk_state(d["X"], d["B"], rAcs.float().to(DEV), dt=dt.to(DEV))
+    assert_close(states, S_ref, 0.0, atol=3e-5 * S_ref.abs().max().item())
+
+
 @pytest.mark.parametrize("state_dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("init", [False, True])
 @pytest.mark.parametrize("nc", [1, 7, 16, 33])

@@ -400,13 +400,19 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
     const T* bl = bs[bf];
     const float* ab = al[bf];
     const float last = ab[Q - 1] * kLog2e;
-    // the chunk's weights, token 64 k + lane by each lane, into this wave's
-    // copy (the same values as forming each lane's 8 weights per K step)
+    // 16-bit inputs, and f32 inputs with several workgroups per CU: the
+    // chunk's weights, token 64 k + lane by each lane, into this wave's copy
+    // (the same values as forming each lane's 8 weights per K step, which f32
+    // inputs with one workgroup per CU still do: there the LDS round trip
+    // would lie on the chain's critical path, C2 110 -> 119 us)
+    constexpr bool kWaveWeights = !std::is_same<T, float>::value || !DB;
     float* wv = wl[wave];
+    if constexpr (kWaveWeights) {
 #pragma unroll
-    for (int k = 0; k < Q / 64; ++k) {
-      const int l = 64 * k + lane;
-      wv[l] = chunk_weight(ab[l], last, HAS_DT ? dl[bf][l] : 1.f);
+      for (int k = 0; k < Q / 64; ++k) {
+        const int l = 64 * k + lane;
+        wv[l] = chunk_weight(ab[l], last, HAS_DT ? dl[bf][l] : 1.f);
+      }
     }
     f32x4 acc[2][NTW];
 #pragma unroll
@@ -418,9 +424,18 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
       float w[8];
 #pragma unroll
       for (int s2 = 0; s2 < 2; ++s2) {
-        const f32x4 w4 = *reinterpret_cast<const f32x4*>(wv + 32 * ks + 16 * s2 + 4 * g);
+        const int l = 32 * ks + 16 * s2 + 4 * g;
+        if constexpr (kWaveWeights) {
+          const f32x4 w4 = *reinterpret_cast<const f32x4*>(wv + l);
 #pragma unroll
-        for (int jj = 0; jj < 4; ++jj) w[4 * s2 + jj] = w4[jj];
+          for (int jj = 0; jj < 4; ++jj) w[4 * s2 + jj] = w4[jj];
+        } else {
+          const f32x4 a4 = *reinterpret_cast<const f32x4*>(ab + l);
+          f32x4 d4 = f32x4{1.f, 1.f, 1.f, 1.f};
+          if constexpr (HAS_DT) d4 = *reinterpret_cast<const f32x4*>(&dl[bf][l]);
+#pragma unroll
+          for (int jj = 0; jj < 4; ++jj) w[4 * s2 + jj] = chunk_weight(a4[jj], last, d4[jj]);
+        }
       }
       BFrag<T> bfr[NTW];
 #pragma unroll
