@@ -222,3 +222,18 @@ def test_layer_entry_points_validate_on_the_host():
     assert fwd(None, n) == -1
     prm.conv_kernel = 7
     assert fwd(fake, n) == -13
+
+
+def test_build_rejects_kernels_with_scratch():
+    """build.py reads hipcc's per-kernel resource remarks and names every
+    kernel that spills registers to scratch (the build then fails)."""
+    from workloadsuite_amd import build
+    text = "\n".join([
+        "a.hip:1:1: remark: Function Name: _Zspill [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:1:1: remark:     VGPRs: 128 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:1:1: remark:     ScratchSize [bytes/lane]: 12 [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:9:1: remark: Function Name: _Zclean [-Rpass-analysis=kernel-resource-usage]",
+        "a.hip:9:1: remark:     ScratchSize [bytes/lane]: 0 [-Rpass-analysis=kernel-resource-usage]",
+    ])
+    assert build._spills(text) == [("_Zspill", 12)]
+    assert "-Rpass-analysis=kernel-resource-usage" in build.RESOURCE_FLAGS

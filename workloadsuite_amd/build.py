@@ -11,6 +11,7 @@ from __future__ import annotations
 
 import concurrent.futures
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -51,17 +52,41 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (ROCm is required to build libssd)")
 
 
+# Every kernel keeps its registers: the compiler's per-kernel resource remarks
+# are read and a kernel with scratch (spilled registers) fails the build.
+RESOURCE_FLAGS = ["-Rpass-analysis=kernel-resource-usage"]
+
+
+def _spills(text: str) -> list:
+    """(kernel, bytes per lane) for every kernel whose remarks report scratch."""
+    out, name = [], None
+    for ln in text.splitlines():
+        m = re.search(r"remark:\s+Function Name: (\S+)", ln)
+        if m:
+            name = m.group(1)
+            continue
+        m = re.search(r"remark:\s+ScratchSize \[bytes/lane\]: (\d+)", ln)
+        if m and name and int(m.group(1)) > 0:
+            out.append((name, int(m.group(1))))
+    return out
+
+
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD, os.path.splitext(src)[0] + ".o")
-    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *COMMON_FLAGS, *DEVICE_FLAGS, *RESOURCE_FLAGS, "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    # The host pass does not know the packed-fp32 target feature; drop that note.
+    text = res.stdout + res.stderr
+    # The host pass does not know the packed-fp32 target feature; drop that
+    # note, and the resource remarks (checked below).
     noise = "'-packed-fp32-ops' is not a recognized feature"
-    msgs = [ln for ln in (res.stdout + res.stderr).splitlines() if noise not in ln]
+    msgs = [ln for ln in text.splitlines() if noise not in ln and "kernel-resource-usage" not in ln]
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src}:\n" + "\n".join(msgs))
+    spills = _spills(text)
+    if spills:
+        raise RuntimeError(f"{src}: kernels spill registers to scratch (bytes per lane): {spills}")
     if verbose and msgs:
         print("\n".join(msgs))
     return obj

@@ -101,7 +101,7 @@ __device__ __forceinline__ f32x4 kstep(const BFrag<T>& bf, const frag8<T>& x, co
     return mma(bf, xf, acc);
   } else {
     frag8<T> hi, lo;
-    split_weighted<T>(x, f32x4{w[0], w[1], w[2], w[3]}, f32x4{w[4], w[5], w[6], w[7]}, hi, lo);
+    split_weighted<T, true>(x, f32x4{w[0], w[1], w[2], w[3]}, f32x4{w[4], w[5], w[6], w[7]}, hi, lo);
     acc = mma(bf, hi, acc);
     return mma(bf, lo, acc);
   }

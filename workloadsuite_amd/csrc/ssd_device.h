@@ -69,22 +69,24 @@ template <typename T> __device__ __forceinline__ float to_f32(T v) { return (flo
 // fma.  Pairs of elements take one packed conversion each way (for bf16 hi's
 // f32 value is read back from its bits): fewer instructions than converting
 // one value at a time, same values.
-// f16: the product b w is formed as an fma with an opaque -0 addend (the
-// same value as the product; the compiler would turn a literal -0 back into a
-// multiply), so that it takes the f16 b as it is (v_fma_mix_f32) instead of
-// converting it first.
-template <typename T>
+// MIX (f16): the product b w is formed as an fma with an opaque -0 addend
+// (the same value as the product; the compiler would turn a literal -0 back
+// into a multiply), so that it takes the f16 b as it is (v_fma_mix_f32)
+// instead of converting it first -- one register more, which the chunk-256
+// state chain does not have to spare.
+template <typename T, bool MIX = false>
 __device__ __forceinline__ void split_weighted(const frag8<T>& b, f32x4 w0, f32x4 w1, frag8<T>& hi, frag8<T>& lo) {
   typedef T t2 __attribute__((ext_vector_type(2)));
   typedef float f32x2 __attribute__((ext_vector_type(2)));
+  constexpr bool kMix = MIX && std::is_same<T, f16>::value;
   float nz = -0.f;
-  if constexpr (std::is_same<T, f16>::value) asm("" : "+v"(nz));
+  if constexpr (kMix) asm("" : "+v"(nz));
 #pragma unroll
   for (int j = 0; j < 8; j += 2) {
     const float wa = j < 4 ? w0[j] : w1[j - 4], wb = j < 4 ? w0[j + 1] : w1[j - 3];
     const float b0 = (float)b[j], b1 = (float)b[j + 1];
-    const float v0 = std::is_same<T, f16>::value ? __builtin_fmaf(b0, wa, nz) : b0 * wa;
-    const float v1 = std::is_same<T, f16>::value ? __builtin_fmaf(b1, wb, nz) : b1 * wb;
+    const float v0 = kMix ? __builtin_fmaf(b0, wa, nz) : b0 * wa;
+    const float v1 = kMix ? __builtin_fmaf(b1, wb, nz) : b1 * wb;
     const t2 h = __builtin_convertvector((f32x2{v0, v1}), t2);
     f32x2 hf;
     if constexpr (std::is_same<T, bf16>::value) {
