@@ -41,7 +41,7 @@
 extern "C" {
 #endif
 
-#define SSD_ABI_VERSION 6
+#define SSD_ABI_VERSION 7
 
 /* Element types.  The SPLIT and F16S values are storage formats of the
  * per-chunk states only, all laid out in the f32 states buffer

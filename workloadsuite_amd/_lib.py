@@ -15,7 +15,7 @@ import torch  # noqa: F401  -- must precede the CDLL, see module docstring
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssd.so")
 
-SSD_ABI_VERSION = 6
+SSD_ABI_VERSION = 7
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 STATE_SPLIT_BF16, STATE_SPLIT_F16 = 3, 4  # f32 states as 16-bit (hi, lo) pairs
 STATE_F16S = 5  # f32 states as f16 rows with a power-of-two scale per row
