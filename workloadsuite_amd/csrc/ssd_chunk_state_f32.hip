@@ -326,7 +326,9 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
     for (int n = 0; n < NTW; ++n)
       st[a][n] = sp.init ? *reinterpret_cast<const f32x4*>(sp.init + bh * PN + sidx(a, n)) : f32x4{0.f, 0.f, 0.f, 0.f};
   // F16S: this wave's part of the row maxima of the running state (lanes
-  // i, i + 16, i + 32, i + 48 hold row p's 16 n of each of its n tiles)
+  // i, i + 16, i + 32, i + 48 hold row p's 16 n of each of its n tiles; two
+  // lane swaps in the VALU, each lane keeping the larger of its value and
+  // the swapped one)
   auto put_rmax = [&](int buf) __attribute__((always_inline)) {
 #pragma unroll
     for (int a = 0; a < 2; ++a) {
@@ -335,8 +337,10 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
       for (int n = 0; n < NTW; ++n)
 #pragma unroll
         for (int k = 0; k < 4; ++k) m = fmaxf(m, fabsf(st[a][n][k]));
-      m = fmaxf(m, __shfl_xor(m, 16));
-      m = fmaxf(m, __shfl_xor(m, 32));
+      const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+      m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+      m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
       if (g == 0) rmax[buf][(wave >> 1) * kP + 16 * (2 * pp + a) + i] = m;
     }
   };
