@@ -61,7 +61,7 @@ def esize(dt):
     return torch.tensor([], dtype=dt).element_size()
 
 
-def kernel_model(cfg, state_dtype, handover=None, local_f16=False):
+def kernel_model(cfg, state_dtype, handover=None, local_f16=False, cb_in_scan=True):
     """Algorithmic HBM bytes and MFMA flops per launch of each kernel.
 
     Bytes count every operand read once and every result written once at its
@@ -71,7 +71,12 @@ def kernel_model(cfg, state_dtype, handover=None, local_f16=False):
     the (hi, lo) pairs taking 4 bytes); the local states between chunk_state
     and state_passing at the state dtype, or (``local_f16``) as f16 with a
     4-byte scale per row and 16-column tile.  Flops count useful work: the
-    causal triangle T_Q = Q(Q+1)/2 of the intra-chunk products.
+    causal triangle T_Q = Q(Q+1)/2 of the intra-chunk products, with C.B^T
+    formed once per (batch, chunk, group) as the kernels form it -- inside
+    chunk_scan (``cb_in_scan``), or in chunk_prep where that runs (16-bit
+    inputs at chunk 256), and then not in chunk_scan.  ``flops_cb_per_head``
+    of chunk_scan is the reference algorithm's count (C.B^T per head after
+    the GQA repeat, MR:97-99, 143), kept as a separately labelled figure.
     """
     b, L, h, P, N, Q, g = cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.chunk, cfg.ngroups
     c = L // Q
@@ -96,7 +101,8 @@ def kernel_model(cfg, state_dtype, handover=None, local_f16=False):
         # K2 + K3 as the forward runs them: x in, S_in out; the local states are not counted
         "chunk_state_passing": dict(bytes=x + bc + acs + dec + sin + fin + init, flops=2 * b * c * h * (Q + 1) * P * N),
         "chunk_scan": dict(bytes=x + 2 * bc + acs + sin + x,
-                           flops=b * c * h * (2 * TQ * N + 2 * TQ * P + 2 * Q * N * P)),
+                           flops=b * c * h * (2 * TQ * P + 2 * Q * N * P) + (b * c * g * 2 * TQ * N if cb_in_scan else 0),
+                           flops_cb_per_head=b * c * h * (2 * TQ * N + 2 * TQ * P + 2 * Q * N * P)),
     }
 
 
@@ -162,6 +168,26 @@ def profiled_traffic(cfg, kernel):
         if line.startswith(key):
             return int(line[len(key):].strip()), os.path.relpath(path, ROOT)
     return None, None
+
+
+def profiled_mfma(cfg, kernel):
+    """MFMA instructions per launch of `kernel` (rocprofv3 SQ_INSTS_MFMA) and
+    the flops one of them performs, as committed under
+    profiles/ssd_forward_<config>.md in lines ``mfma_instructions_per_launch
+    <kernel>: <n>`` and ``mfma_flops_per_instruction <kernel>: <f>``;
+    None when there is no such measurement."""
+    path = os.path.join(ROOT, "profiles", f"ssd_forward_{cfg.name}.md")
+    if not os.path.exists(path):
+        return None
+    got = {}
+    for line in open(path):
+        for key in ("mfma_instructions_per_launch", "mfma_flops_per_instruction"):
+            k = f"{key} {kernel}:"
+            if line.startswith(k):
+                got[key] = int(line[len(k):].strip())
+    if len(got) != 2:
+        return None
+    return got["mfma_instructions_per_launch"] * got["mfma_flops_per_instruction"]
 
 
 def summarize(samples):
@@ -241,6 +267,69 @@ def cpu_baseline(cfg, budget_s=12.0, max_runs=30):
     }
 
 
+def hbm_probe(args):
+    """The streaming probes of libssd_probe.so (csrc/ssd_probe.hip): read
+    args.hbm_probe MiB of f32 with 16-byte loads and write one f16 per f32
+    read (state_passing's 2 : 1 read / write mix, 8-byte or 16-byte stores),
+    or copy them (1 : 1); plain or non-temporal loads and stores, 4 or 8
+    vectors in flight per thread, 4 / 8 / 16 workgroups of 256 threads per
+    CU.  Two source / destination pairs are used in turn, together well
+    beyond the 256 MB Infinity Cache.  Reports every variant, the best per
+    mix, and torch's own device copy for reference."""
+    import ctypes
+
+    lib = ctypes.CDLL(os.path.join(ROOT, "workloadsuite_amd", "libssd_probe.so"))
+    lib.ssd_stream_probe.restype = ctypes.c_int
+    lib.ssd_stream_probe.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
+                                     ctypes.c_int, ctypes.c_void_p]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+    n = (args.hbm_probe << 20) // 4
+    src = [torch.rand(n, device=dev) for _ in range(2)]
+    dst = [torch.empty(n, dtype=torch.float32, device=dev) for _ in range(2)]
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    out = {"hbm_probe_read_bytes": 4 * n, "peak_GB_s": PEAK_HBM_GBS, "reps": args.kernel_reps, "probes": {},
+           "best": {}}
+    mixes = {0: "2:1 mix, f16x4 stores", 1: "2:1 mix, f16x8 stores", 2: "copy 1:1"}
+    for kind in (0, 1, 2):
+        for flags in range(8):
+            for per_cu in (4, 8, 16):
+                k = [0]
+
+                def launch():
+                    i = k[0] % 2
+                    k[0] += 1
+                    rc = lib.ssd_stream_probe(ctypes.c_void_p(src[i].data_ptr()), ctypes.c_void_p(dst[i].data_ptr()),
+                                              n, kind, flags, per_cu * cus, stream)
+                    if rc:
+                        raise RuntimeError(f"ssd_stream_probe failed: {rc}")
+
+                launch()
+                ms = time_launches(launch, args.kernel_reps)
+                moved = 4 * n + (4 * n if kind == 2 else 2 * n)
+                gbs = moved / (ms * 1e-3) / 1e9
+                name = (f"{mixes[kind]}, {'nt' if flags & 1 else 'plain'} loads, {'nt' if flags & 2 else 'plain'} "
+                        f"stores, {8 if flags & 4 else 4} in flight, {per_cu} WG/CU")
+                out["probes"][name] = {"ms": round(ms, 5), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+                best = out["best"].get(mixes[kind])
+                if best is None or gbs > best["GB_s"]:
+                    out["best"][mixes[kind]] = {"variant": name, "GB_s": round(gbs, 1),
+                                                "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+    k = [0]
+
+    def torch_copy():
+        i = k[0] % 2
+        k[0] += 1
+        dst[i].copy_(src[i])
+
+    torch_copy()
+    ms = time_launches(torch_copy, args.kernel_reps)
+    gbs = 8 * n / (ms * 1e-3) / 1e9
+    out["torch_copy"] = {"ms": round(ms, 5), "GB_s": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)}
+    print(json.dumps(out), flush=True)
+
+
 def layer_bench(args):
     import torch.nn.functional as F
 
@@ -317,6 +406,10 @@ def main():
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="only run a plain device-to-device copy of MB MiB (5 times) and exit: the "
                          "reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
+    ap.add_argument("--hbm-probe", type=int, default=0, metavar="MB",
+                    help="only time the hand-written streaming probes (libssd_probe.so) reading MB MiB of f32 "
+                         "at state_passing's read / write mix (and a copy), with and without non-temporal "
+                         "loads, and exit with one JSON line")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -327,6 +420,10 @@ def main():
 
     if args.layer:
         layer_bench(args)
+        return
+
+    if args.hbm_probe:
+        hbm_probe(args)
         return
 
     if args.copy_probe:
@@ -345,19 +442,25 @@ def main():
     torch.cuda.set_device(dev)
     inp = make_inputs(cfg, seed=0, device=dev)
     X, A, B, C, init = inp["X"], inp["A"], inp["B"], inp["C"], inp["init"]
+    # the chunk ssd_forward runs this config at (16-bit inputs at chunk 64 /
+    # 128 run at 256 where seqlen and d_state allow): the kernels are timed,
+    # and their traffic modelled, at that chunk
+    run_chunk = S.forward_chunk(cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, cfg.chunk,
+                                cfg.dtype, state_dtype, args.state_format)
+    kcfg = cfg.scaled(chunk=run_chunk)
 
     # ---- per-kernel device time, each kernel on its real inputs ----
-    Acs, decay = S.chunk_cumsum(A, cfg.chunk)
-    prep = S.chunk_prep(B, C, cfg.chunk)
+    Acs, decay = S.chunk_cumsum(A, kcfg.chunk)
+    prep = S.chunk_prep(B, C, kcfg.chunk)
     states = S.chunk_state(X, B, Acs, state_dtype=state_dtype, prep=prep)
     # as in ssd_forward: with 16-bit inputs and f32 states, K3 hands S_in to K4
     # as f16 rows with a power-of-two scale per row ("f16s"), or at chunk 256
     # as 16-bit (hi, lo) pairs with --state-format split
-    split = handover_format(cfg, state_dtype, prep, args.state_format)
+    split = handover_format(kcfg, state_dtype, prep, args.state_format)
     # where the forward runs chunk_state then state_passing with the f16s
     # hand-over at chunk 256, the local states cross HBM as f16 rows: time
     # those variants
-    local_f16 = split == "f16s" and prep is not None and not takes_state_chain(cfg, split, state_dtype)
+    local_f16 = split == "f16s" and prep is not None and not takes_state_chain(kcfg, split, state_dtype)
     if local_f16:
         states = S.chunk_state(X, B, Acs, state_dtype="f16s", prep=prep).states
     S_in, _ = S.state_passing(S.F16SLocalStates(states) if local_f16 else states, decay, init, split=split)
@@ -379,8 +482,8 @@ def main():
 
     sp_final = torch.empty(cfg.batch, cfg.nheads, cfg.headdim, cfg.dstate, device=dev) if cfg.final_state else None
     kfn = {
-        "chunk_cumsum": lambda: S.chunk_cumsum(A, cfg.chunk),
-        "chunk_prep": lambda: S.chunk_prep(B, C, cfg.chunk),
+        "chunk_cumsum": lambda: S.chunk_cumsum(A, kcfg.chunk),
+        "chunk_prep": lambda: S.chunk_prep(B, C, kcfg.chunk),
         "chunk_state": lambda: S.chunk_state(X, B, Acs, state_dtype="f16s" if local_f16 else state_dtype, prep=prep),
         "state_passing": sp_launch,
         "chunk_state_passing": lambda: S.chunk_state_passing(X, B, Acs, decay, prep=prep, initial_states=init,
@@ -391,11 +494,14 @@ def main():
     }
     if prep is None:
         del kfn["chunk_prep"]
-    model = kernel_model(cfg, state_dtype, split if isinstance(split, str) else None, local_f16)
+    model = kernel_model(kcfg, state_dtype, split if isinstance(split, str) else None, local_f16,
+                         cb_in_scan=prep is None)
     kernels = {}
+    pre_launches = 0
     for name, fn in kfn.items():
         fn()
         ms = time_launches(fn, args.kernel_reps)
+        pre_launches += 1 + args.kernel_reps
         m = model[name]
         gbs = m["bytes"] / (ms * 1e-3) / 1e9
         tfs = m["flops"] / (ms * 1e-3) / 1e12
@@ -407,6 +513,15 @@ def main():
             "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "mfma_frac": round(tfs / PEAK_TFLOPS[cfg.dtype], 4),
             "bound": "hbm" if t_hbm >= t_mfma else "mfma",
         }
+        if "flops_cb_per_head" in m:
+            kernels[name]["flops_cb_per_head"] = m["flops_cb_per_head"]
+            kernels[name]["mfma_frac_cb_per_head"] = round(
+                m["flops_cb_per_head"] / (ms * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype], 4)
+        executed = profiled_mfma(cfg, name)
+        if executed is not None:
+            # the flops the MFMA instructions of one launch perform (rocprofv3
+            # SQ_INSTS_MFMA), over this run's time
+            kernels[name]["mfma_executed_frac"] = round(executed / (ms * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype], 4)
     # the dominant kernel among those the forward runs: K2 + K3 as it runs them
     # (chunk_state_passing), K4, K1 and K0 -- not the standalone chunk_state
     # and state_passing rows, which stand in for it only as a breakdown
@@ -419,6 +534,10 @@ def main():
         roof = {"bound": "mfma", "achieved": kd["TFLOP_s"], "peak": PEAK_TFLOPS[cfg.dtype], "unit": "TFLOP/s",
                 "frac": kd["mfma_frac"]}
     roof["kernel"] = dom
+    if roof["bound"] == "mfma":
+        roof["flops_basis"] = "useful: causal triangle, C.B^T once per (batch, chunk, group)"
+        if "mfma_executed_frac" in kd:
+            roof["mfma_executed_frac"] = kd["mfma_executed_frac"]
     roof["traffic"], roof["traffic_source"] = profiled_traffic(cfg, dom)
 
     # ---- K forwards timed one by one: per-step median / mean / p90 / p99 ----
@@ -432,6 +551,7 @@ def main():
                              state_format=args.state_format)
 
     stats = step_stats(step, args.steps)
+    pre_launches_forwards = args.steps
 
     # ---- the headline: W warmup steps, then K whole forwards back to back ----
     for _ in range(args.warmup):
@@ -467,15 +587,21 @@ def main():
         "data": "synthetic (seeded: X~N(0,1), B,C~N(0,1)/sqrt(N), A=-softplus(N(-2,1))*exp(N(0,.5)))",
         "config": {"workload": f"mamba2-ssd-forward {cfg.name}" + (" (Mamba-2-2.7B layer)" if cfg.name == "C3" else ""),
                    "batch": cfg.batch, "seqlen": cfg.seqlen, "nheads": cfg.nheads, "headdim": cfg.headdim,
-                   "dstate": cfg.dstate, "chunk": cfg.chunk, "ngroups": cfg.ngroups,
+                   "dstate": cfg.dstate, "chunk": cfg.chunk, "chunk_run": run_chunk, "ngroups": cfg.ngroups,
                    "inputs": f"{DTYPE_NAMES[cfg.dtype]} X/B/C, f32 A", "state_storage": args.state_dtype,
                    "state_handover": split if isinstance(split, str) else ("split" if split is not None else None),
                    "local_states": ("f16 rows" if local_f16 else
-                                    "in registers (state chain)" if takes_state_chain(cfg, split, state_dtype)
+                                    "in registers (state chain)" if takes_state_chain(kcfg, split, state_dtype)
                                     else args.state_dtype),
                    "final_state": cfg.final_state, "initial_state": cfg.init_state},
         "device_ms_per_step": round(dev_ms, 5),
         "step_stats": stats,
+        # what ran on the GPU in this process before the timed region: the
+        # per-kernel timing launches, the step_stats forwards, then the
+        # warmup forwards
+        "pre_timing": {"kernel_launches": pre_launches, "step_stats_forwards": pre_launches_forwards,
+                       "warmup_forwards": args.warmup,
+                       "effective_warmup_forwards": pre_launches_forwards + args.warmup},
         "roofline": roof,
         "end_to_end": {"F_min_per_token": f_min / cfg.tokens, "B_min_per_token": b_min / cfg.tokens,
                        "roofline_tokens_per_s": roof_tps, "frac": round(tokens_per_s / roof_tps, 4)},

@@ -13,12 +13,24 @@
  *   - Strides are in ELEMENTS; the innermost dimension must have stride 1.
  *   - `stream` is a hipStream_t (NULL = the default stream).  Every kernel is
  *     launched on it; nothing synchronises the host.
- *   - The library allocates nothing, frees nothing and keeps no pointer past
- *     the call: the caller owns every buffer, workspaces included.
+ *   - Except ssd_forward_noalloc, no entry point allocates or frees device
+ *     memory or keeps a pointer past the call: the caller owns every buffer,
+ *     workspaces included.  ssd_forward_noalloc's workspace is a static
+ *     __device__ array of SSD_NOALLOC_SCRATCH_BYTES (256 MiB) in the
+ *     library's code object, so every device on which any libssd kernel
+ *     loads holds it from then until the process ends, whether or not the
+ *     process ever calls ssd_forward_noalloc.
  *   - Return value: 0 on success, a negative SSD_ERR_* for invalid arguments
  *     (checked on the host before any launch), a positive hipError_t when a
  *     launch fails.  ssd_strerror() names both.  No exit/abort in the library.
- *   - Thread-safe and re-entrant: no global mutable state.
+ *   - Thread-safe and re-entrant.  Host-side state: a per-device cache of the
+ *     CU count (the state chain's launch plan), and ssd_forward_noalloc's
+ *     per-device cache of its array's device address (behind a mutex; stale
+ *     after hipDeviceReset).  Calls of ssd_forward_noalloc that overlap on
+ *     one device race on its array.
+ *   - Operands copied to LDS 16 bytes at a time (x, bmat, cmat, a_cumsum,
+ *     states, initial / final states) need 16-byte aligned bases and rows;
+ *     SSD_ERR_MISALIGNED otherwise.
  *
  * Layouts (b batch, L seqlen, h heads, P headdim, N dstate, g groups,
  *          Q chunk, c = L / Q chunks):
@@ -41,7 +53,7 @@
 extern "C" {
 #endif
 
-#define SSD_ABI_VERSION 7
+#define SSD_ABI_VERSION 8
 
 /* Element types.  The SPLIT and F16S values are storage formats of the
  * per-chunk states only, all laid out in the f32 states buffer
@@ -69,7 +81,14 @@ extern "C" {
  * at chunk 256 and dstate 64 / 128.  ssd_forward hands the states to
  * chunk_scan as F16S wherever that applies (state_dtype SSD_DTYPE_F32), or in
  * the format state_dtype names (at chunk 256; a SPLIT state_dtype at chunk
- * 64 / 128 hands over plain f32). */
+ * 64 / 128 hands over plain f32).
+ * Where the forward runs chunk_state and state_passing as separate launches
+ * with an F16S hand-over (16-bit inputs at chunk 256 outside the one-launch
+ * state chain, and the chain's segments), the local states cross HBM as
+ * F16S_LOCAL; the chain keeps them in f32 registers.  So the forward's last
+ * bits depend on the launch plan, which depends on batch x heads and the
+ * device's CU count: results are not bitwise invariant to batch slicing.
+ * state_dtype SPLIT (at chunk 256) keeps every local state in f32. */
 enum {
   SSD_DTYPE_F32 = 0,
   SSD_DTYPE_BF16 = 1,
@@ -89,7 +108,7 @@ enum {
   SSD_ERR_HEADS_NOT_DIVISIBLE = -4,  /* h % g != 0 (MR:37-38 raises)           */
   SSD_ERR_UNSUPPORTED_DTYPE = -5,
   SSD_ERR_UNSUPPORTED_HEADDIM = -6,  /* P != 64                                */
-  SSD_ERR_UNSUPPORTED_DSTATE = -7,   /* N not in {16, 32, 64, 128, 256}        */
+  SSD_ERR_UNSUPPORTED_DSTATE = -7,   /* N not in {16, 32, 64, 128}             */
   SSD_ERR_UNSUPPORTED_CHUNK = -8,    /* Q not in {64, 128, 256}                */
   SSD_ERR_BAD_STRIDE = -9,           /* innermost stride != 1, or negative     */
   SSD_ERR_MISALIGNED = -10,          /* vector-loaded rows not 16-byte aligned */
@@ -236,7 +255,20 @@ int ssd_chunk_scan(const ssd_dims* d, int dtype,
 
 /* Whole SSD forward (K1, K0, K2, K3, K4 on one stream): the replacement for
  * SSDLayer._ssd_core (MR:123-162).  workspace must hold
- * ssd_workspace_bytes(d, state_dtype) bytes, 256-byte aligned. */
+ * ssd_workspace_bytes(d, state_dtype) bytes, 256-byte aligned (or that of
+ * the chunk ssd_forward_chunk reports).  d->chunk is MR's block_len and only
+ * has to divide L: for 16-bit inputs with f32 states (SSD_DTYPE_F32 or
+ * SSD_STATE_F16S), L % 256 == 0 and dstate 64 / 128, a chunk of 64 or 128
+ * runs at 256 unless that workspace would be larger than the caller's
+ * chunk's (see ssd_forward_chunk).  Every chunking evaluates the same linear
+ * recurrence (MR:152-161), so this changes rounding only. */
+/* The chunk length ssd_forward (and ssd_forward_noalloc) runs d at for this
+ * dtype and state_dtype: d->chunk, or 256 where the rule above applies; 0
+ * for invalid dims.  Host-only.  No counterpart in the reference (its
+ * block_len is the chunk); for callers that size the workspace at the chunk
+ * actually run or time its kernels one by one. */
+int64_t ssd_forward_chunk(const ssd_dims* d, int dtype, int state_dtype);
+
 int ssd_forward(const ssd_dims* d, int dtype,
                 const void* x, const int64_t x_strides[4],
                 const float* a, const int64_t a_strides[3],
@@ -324,17 +356,21 @@ int ssd_layer_forward(const ssd_dims* d, int dtype, const ssd_layer_params* prm,
                       void* y, const int64_t y_strides[3],
                       void* workspace, size_t workspace_bytes, void* stream);
 
-/* ssd_forward without a workspace argument: the workspace is a device array
- * of SSD_NOALLOC_SCRATCH_BYTES that the library keeps per device (from its
- * first use on that device until the process ends), so the call itself
- * allocates nothing.  No counterpart in the reference: it is for callers that
- * cannot allocate device memory (code under HIP graph capture, tight serving
- * loops, harnesses that forbid hipMalloc).  Same arguments and results as
- * ssd_forward otherwise; the caller still provides every input and output.
- * When the workspace of the whole call (ssd_workspace_bytes) is larger than
- * the array, the batch runs in slices whose workspace fits; a shape whose
- * single batch element needs more returns SSD_ERR_WORKSPACE_TOO_SMALL before
- * any launch.  All calls on one device share that device's array: calls that
+/* ssd_forward without a workspace argument: the workspace is a static
+ * __device__ array of SSD_NOALLOC_SCRATCH_BYTES in libssd's code object, so
+ * the call itself allocates nothing.  The array is reserved on every device
+ * where the code object loads (any libssd kernel launch loads it), until the
+ * process ends, whether or not ssd_forward_noalloc is ever called.  Its
+ * device address is looked up once per device (hipGetSymbolAddress) and
+ * cached on the host; after a hipDeviceReset that cache is stale.  No
+ * counterpart in the reference: it is for callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc).  Same arguments and results as ssd_forward otherwise,
+ * at the chunk ssd_forward_chunk reports; the caller still provides every
+ * input and output.  When the workspace of the whole call is larger than the
+ * array, the batch runs in slices whose workspace fits; a shape whose single
+ * batch element needs more returns SSD_ERR_WORKSPACE_TOO_SMALL before any
+ * launch.  All calls on one device share that device's array: calls that
  * overlap on one device (other streams, other threads) race, so the caller
  * serialises them. */
 #define SSD_NOALLOC_SCRATCH_BYTES ((size_t)256 << 20)

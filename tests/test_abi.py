@@ -237,3 +237,91 @@ def test_build_rejects_kernels_with_scratch():
     ])
     assert build._spills(text) == [("_Zspill", 12)]
     assert "-Rpass-analysis=kernel-resource-usage" in build.RESOURCE_FLAGS
+
+
+def test_forward_chunk_routes_16bit_small_chunks_to_256():
+    """ssd_forward_chunk: the chunk ssd_forward runs at.  16-bit inputs with
+    f32 states (or F16S), L % 256 == 0 and dstate 64 / 128 run chunk 64 / 128
+    at 256, unless that workspace would be the larger one (B and C given per
+    head, as MR's _ssd_core passes them after the repeat: chunk_prep's
+    per-group operands then outgrow the states saved)."""
+    lib = _lib.load()
+    q = lambda dtype, sd=_lib.DTYPE_F32, **kw: lib.ssd_forward_chunk(ctypes.byref(r0(**kw)), dtype, sd)  # noqa: E731
+    assert q(_lib.DTYPE_F16) == 256 and q(_lib.DTYPE_BF16) == 256
+    assert q(_lib.DTYPE_F16, _lib.STATE_F16S) == 256
+    assert q(_lib.DTYPE_F16, chunk=128) == 256 and q(_lib.DTYPE_F16, chunk=256) == 256
+    assert q(_lib.DTYPE_F32) == 64                                   # no chunk-256 f32 path
+    assert q(_lib.DTYPE_F16, seqlen=2048 + 64) == 64                 # L % 256 != 0
+    assert q(_lib.DTYPE_F16, dstate=32) == 64                        # not a persistent-kernel shape
+    assert q(_lib.DTYPE_F16, _lib.DTYPE_BF16) == 64                  # bf16 states keep the chunk
+    assert q(_lib.DTYPE_F16, _lib.STATE_SPLIT_F16) == 64             # so does the split format
+    assert q(_lib.DTYPE_F16, ngroups=128) == 64                      # per-head B / C (MR's _ssd_core)
+    assert q(_lib.DTYPE_F16, seqlen=100) == 0                        # invalid dims
+    # routed only where the chunk-256 workspace is not larger than the caller's
+    for g in (1, 8, 32, 64, 128):
+        dims = r0(ngroups=g)
+        d256 = r0(ngroups=g, chunk=256)
+        n64 = lib.ssd_workspace_bytes(ctypes.byref(dims), _lib.DTYPE_F32)
+        n256 = lib.ssd_workspace_bytes(ctypes.byref(d256), _lib.DTYPE_F32)
+        assert lib.ssd_forward_chunk(ctypes.byref(dims), _lib.DTYPE_F16, 0) == (256 if n256 <= n64 else 64)
+
+
+def r0(**kw):
+    """R0's dims (MR's defaults: batch 8, seqlen 2048, 128 heads, d_state 128, 8 groups, block_len 64)."""
+    base = dict(batch=8, seqlen=2048, nheads=128, headdim=64, dstate=128, ngroups=8, chunk=64)
+    base.update(kw)
+    return _lib.SSDDims(*[base[k] for k in ("batch", "seqlen", "nheads", "headdim", "dstate", "ngroups", "chunk")])
+
+
+def test_forward_workspace_check_uses_the_chunk_it_runs_at():
+    """A routed forward accepts a workspace sized for chunk 256 (smaller than
+    chunk 64's) and rejects one byte less; rejected on the host before any launch."""
+    lib = _lib.load()
+    dims = r0()
+    n256 = lib.ssd_workspace_bytes(ctypes.byref(r0(chunk=256)), _lib.DTYPE_F32)
+    assert n256 < lib.ssd_workspace_bytes(ctypes.byref(dims), _lib.DTYPE_F32)
+    s4 = (ctypes.c_int64 * 4)(2048 * 128 * 64, 128 * 64, 64, 1)
+    s3 = (ctypes.c_int64 * 3)(2048 * 128, 128, 1)
+    bs4 = (ctypes.c_int64 * 4)(2048 * 8 * 128, 8 * 128, 128, 1)
+    fake = ctypes.c_void_p(0x100000)
+    # every operand valid but y misaligned: the workspace check passes first at n256
+    rc = lib.ssd_forward(ctypes.byref(dims), _lib.DTYPE_F16, fake, s4, fake, s3, fake, bs4, fake, bs4, None, None,
+                         None, ctypes.c_void_p(0x100002), s4, None, fake, n256, 0, None)
+    assert rc == -10
+    rc = lib.ssd_forward(ctypes.byref(dims), _lib.DTYPE_F16, fake, s4, fake, s3, fake, bs4, fake, bs4, None, None,
+                         None, fake, s4, None, fake, n256 - 1, 0, None)
+    assert rc == -11
+
+
+def test_per_kernel_entry_points_reject_misaligned_cumsum_and_states():
+    """a_cumsum and the states are copied to LDS 16 bytes at a time: a base
+    that is only 4-byte aligned is rejected (SSD_ERR_MISALIGNED) on the host."""
+    lib = _lib.load()
+    dims = d()
+    s4 = (ctypes.c_int64 * 4)(256 * 8 * 64, 8 * 64, 64, 1)
+    bs4 = (ctypes.c_int64 * 4)(256 * 2 * 64, 2 * 64, 64, 1)
+    ys4 = (ctypes.c_int64 * 4)(256 * 8 * 64, 8 * 64, 64, 1)
+    fake = ctypes.c_void_p(0x100000)
+    mis = ctypes.c_void_p(0x100004)
+    # ssd_chunk_state: a_cumsum, then states
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, mis, fake, 0, None, None) == -10
+    assert lib.ssd_chunk_state(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, fake, mis, 0, None, None) == -10
+    # ssd_chunk_state_passing: a_cumsum
+    assert lib.ssd_chunk_state_passing(ctypes.byref(dims), 1, fake, s4, fake, bs4, None, None, mis, fake, None, None,
+                                       fake, 0, None, None, None) == -10
+    # ssd_chunk_scan: a_cumsum, then states
+    scan = lambda acs, st: lib.ssd_chunk_scan(ctypes.byref(dims), 1, fake, s4, fake, bs4, fake, bs4, None, None,  # noqa: E731
+                                              acs, st, 0, None, fake, ys4, None, None, None)
+    assert scan(mis, fake) == -10
+    assert scan(fake, mis) == -10
+
+
+def test_forward_chunk_keeps_the_chunk_where_chunk_prep_outweighs_the_states_saved():
+    """C5-like 16-bit shape (8 groups, d_state 64, chunk 128): chunk_prep's
+    per-group operands at chunk 256 take more than the halved states save,
+    so the forward keeps chunk 128; with 4 groups it runs at 256."""
+    lib = _lib.load()
+    keep = _lib.SSDDims(8, 512, 64, 64, 64, 8, 128)
+    move = _lib.SSDDims(8, 512, 64, 64, 64, 4, 128)
+    assert lib.ssd_forward_chunk(ctypes.byref(keep), _lib.DTYPE_BF16, 0) == 128
+    assert lib.ssd_forward_chunk(ctypes.byref(move), _lib.DTYPE_BF16, 0) == 256

@@ -46,6 +46,9 @@ SHAPES = {
     "C5": (64, 512, 64, 64, 64, 128, 8, False),
     "R0": (8, 2048, 128, 64, 128, 64, 8, True),        # the module's core at chunk 64
     "R0-layer": (8, 2048, 128, 64, 128, 256, 8, True),  # the layer span at chunk 256
+    # MR's _ssd_core arguments (B / C repeated per head, MR:97-99): one group
+    # per head, which ssd_forward keeps at chunk 64
+    "R0-repeated": (8, 2048, 128, 64, 128, 64, 128, True),
 }
 
 _src_cache = {}
@@ -388,7 +391,7 @@ def f32_units(B, L, H, Q, G):
     return h0, h1
 
 
-@pytest.mark.parametrize("name", ["C2", "C5", "R0"])
+@pytest.mark.parametrize("name", ["C2", "C5", "R0", "R0-repeated"])
 def test_f32_kernel_addresses(name):
     B, L, H, P, N, Q, G, _ = SHAPES[name]
     assert P == 64 and Q in (64, 128) and N in (64, 128)
@@ -695,7 +698,7 @@ def test_state_passing_addresses(name):
         "const int row = v / TPR, col = SPT * (v % TPR);",
         "float* elem = base + SPT * (int64_t)v;",
         "*reinterpret_cast<H*>(hrow + c * 2 * cstride) = hv;",
-        "constexpr int spt = 4;",
+        "constexpr int spt = 8, unroll = 2;",
         "const int c = min(c0 + u, nchunks - 1);",
         "const float* rscale = base + f16l_scale_slot<N>(row, col / 16);",
         "const H* q = reinterpret_cast<const H*>(hrow + c * 2 * cstride);",
@@ -703,7 +706,7 @@ def test_state_passing_addresses(name):
     PN = P * N
     nc = L // Q
     chains = B * H
-    for per_thread in (4,):  # f32 / split kernels and the f16s kernel (spt)
+    for per_thread in (4, 8):  # f32 / split kernels (4) and the f16s kernel (spt)
         vec = PN // per_thread
         bpb = -(-vec // 256)
         blocks = np.arange(chains * bpb)
@@ -720,8 +723,8 @@ def test_state_passing_addresses(name):
             # f16 local states in: the same f16 slots, and the row's packed scale
             inside("f16 local scale slot", f16l_scale_slot(row, col // 16, N), 0, PN)
             assert ((col + per_thread - 1) // 16 == col // 16).all()
-    # the chunk index every (clamped) load of the pipelined chain uses (batches of 4 or 8)
-    for unroll in (4, 8):
+    # the chunk index every (clamped) load of the pipelined chain uses (batches of 2, 4 or 8)
+    for unroll in (2, 4, 8):
         for nchunks in sorted({1, 2, 7, 16, 17, nc}):
             c0 = np.arange(0, nchunks + 2 * unroll, unroll)
             c = np.minimum(c0[:, None] + np.arange(unroll)[None, :], nchunks - 1)

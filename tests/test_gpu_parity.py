@@ -433,13 +433,104 @@ def test_config_full_size(name, batches, heads):
     assert_close(fg, fr, tol)
 
 
+def mr_regime_inputs(cfg, seed):
+    """R0-shaped inputs in MR's own parameter regime (MR:61-63, 94, 102-103):
+    A = -(1..h) (A_log = log(1..h)), dt = softplus(dt_raw - 4) with dt_raw,
+    x, B and C ~ N(0, 1/3) (in_proj's default-initialised outputs on a
+    unit-RMS input; x a conv + SiLU output of the same scale), so per-token
+    log-decays A dt reach ~-2.3 at head 127 and the in-chunk cumsums ~-150 at
+    block_len 64 (~-600 at 256).  f16 like MR.  Returns X, A_dt, B, C, dt
+    on the GPU."""
+    b, L, h, P, N, g = cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    sd = 3 ** -0.5
+    X = (torch.randn(b, L, h, P, device=DEV, generator=gen) * sd).half()
+    Bm = (torch.randn(b, L, g, N, device=DEV, generator=gen) * sd).half()
+    Cm = (torch.randn(b, L, g, N, device=DEV, generator=gen) * sd).half()
+    dt_raw = (torch.randn(b, L, h, device=DEV, generator=gen) * sd).half()
+    dt = torch.nn.functional.softplus(dt_raw.float() - 4.0)
+    A = -torch.arange(1, h + 1, device=DEV, dtype=torch.float32)
+    return X, A * dt, Bm, Cm, dt
+
+
+# every group (16 heads each), both ends of A = -(1..128)
+R0_HEADS = [0, 17, 34, 51, 68, 85, 102, 127]
+
+
+def _check_mr_regime(Y, final, X, A, B, C, dt, heads, batches, block_len, ngroups, nheads):
+    bs, hs = torch.tensor(batches), torch.tensor(heads)
+    grp = torch.tensor([hh // (nheads // ngroups) for hh in heads])
+    cpu = lambda t: t.cpu()[bs]  # noqa: E731
+    Yr, fr = O.ssd_chunked(cpu(X)[:, :, hs], cpu(A)[:, :, hs], cpu(B)[:, :, grp], cpu(C)[:, :, grp], block_len,
+                           dt=cpu(dt)[:, :, hs])
+    assert torch.isfinite(Y).all() and torch.isfinite(final).all()
+    assert_close(Y.cpu()[bs][:, :, hs], Yr, 2e-2)
+    assert_close(final.cpu()[bs][:, hs], fr, 2e-2)
+
+
+def test_full_r0_forward_at_block_len_64_in_the_reference_regime():
+    """R0 (batch 8, seqlen 2048, 128 heads, d_state 128, 8 groups, MR's
+    block_len 64, f16) through ssd_forward with MR's own A and dt (see
+    mr_regime_inputs) and B / C per group, the form INTEGRATION's
+    "better" binding passes: the library runs it at chunk 256 (the
+    persistent kernels, in-chunk log-decay sums to ~-600).  Sampled heads
+    of every group on two batches against the float64 oracle at block_len
+    64, 2e-2, Y and the final state."""
+    cfg = CONFIGS["R0"]
+    say("R0 forward, MR regime", cfg)
+    X, A, B, C, dt = mr_regime_inputs(cfg, seed=21)
+    assert S.forward_chunk(cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, 64,
+                           torch.float16) == 256
+    Y, final = S.ssd_forward(X, A, B, C, 64, dt=dt, return_final_states=True)
+    torch.cuda.synchronize()
+    _check_mr_regime(Y, final, X, A, B, C, dt, R0_HEADS, [0, 7], 64, cfg.ngroups, cfg.nheads)
+
+
+def test_full_r0_ssd_core_on_the_block_64_kernels_in_the_reference_regime():
+    """The same inputs through ssd_core with MR's own argument layout
+    (chunked tensors, B / C repeated per head, MR:97-110): with one group
+    per head the chunk-256 workspace would be the larger one, so the library
+    runs MR's block_len 64 itself -- the f32-state chain (f16 rows handed to
+    chunk_scan) and the 16-bit chunk_scan for f32 states, with in-chunk
+    log-decay sums to ~-150.  Sampled heads of every group, 2e-2."""
+    cfg = CONFIGS["R0"]
+    say("R0 ssd_core, MR regime", cfg)
+    b, L, h, P, N, g, Q = cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, 64
+    X, A, B, C, dt = mr_regime_inputs(cfg, seed=21)
+    assert S.forward_chunk(b, L, h, P, N, h, Q, torch.float16) == Q
+    r = h // g
+    chunk = lambda t: t.reshape(b, L // Q, Q, *t.shape[2:])  # noqa: E731
+    Brep = B.repeat_interleave(r, dim=2)
+    Crep = C.repeat_interleave(r, dim=2)
+    Yc = S.ssd_core(chunk(X), chunk(Brep), chunk(Crep), chunk(dt), chunk(A), b)
+    del Brep, Crep
+    torch.cuda.synchronize()
+    Y = Yc.reshape(b, L, h, P)
+    bs, hs = torch.tensor([0, 7]), torch.tensor(R0_HEADS)
+    grp = torch.tensor([hh // r for hh in R0_HEADS])
+    cpu = lambda t: t.cpu()[bs]  # noqa: E731
+    Yr, _ = O.ssd_chunked(cpu(X)[:, :, hs], cpu(A)[:, :, hs], cpu(B)[:, :, grp], cpu(C)[:, :, grp], Q,
+                          dt=cpu(dt)[:, :, hs])
+    assert torch.isfinite(Y).all()
+    assert_close(Y.cpu()[bs][:, :, hs], Yr, 2e-2)
+
+
+def forward_by_kernels(X, A, B, C, Q, dt=None, initial_states=None):
+    """The 16-bit forward at exactly chunk Q (64 / 128) through the per-kernel
+    entry points, as ssd_forward runs that chunk: K1, K2 + K3 handing S_in
+    over as f16 rows ("f16s"), K4 -> (Y, final state)."""
+    Acs, decay = S.chunk_cumsum(A, Q)
+    S_in, final = S.chunk_state_passing(X, B, Acs, decay, dt=dt, initial_states=initial_states, split="f16s")
+    return S.chunk_scan(X, B, C, Acs, S_in, dt=dt, split="f16s"), final
+
+
 @pytest.mark.parametrize("name", ["C3", "C4"])
 def test_full_size_chunk_invariance_and_state_linearity(name):
     """Size-independent properties of the whole forward at the full config
     size (the oracle is too slow there): the chunked SSD computes one linear
     recurrence whatever the chunk length (MR:152-161), so the chunk-256
     persistent path (state chain, chunk_scan's persistent kernel) and the
-    chunk-64 generic kernels agree; and Y is linear in the initial state,
+    chunk-64 kernels agree; and Y is linear in the initial state,
     Y(X, S0) = Y(X, 0) + Y(0, S0), as is the final state.  Tolerances are the
     16-bit one relative to each output's scale (every Y is rounded to bf16
     once)."""
@@ -450,7 +541,9 @@ def test_full_size_chunk_invariance_and_state_linearity(name):
     gen = torch.Generator(device=DEV).manual_seed(4)
     S0 = 0.1 * torch.randn(cfg.batch, cfg.nheads, cfg.headdim, cfg.dstate, device=DEV, generator=gen)
     Y256, f256 = S.ssd_forward(X, A, B, C, 256, return_final_states=True)
-    Y64, f64 = S.ssd_forward(X, A, B, C, 64, return_final_states=True)
+    # ssd_forward itself runs these 16-bit shapes at chunk 256 for any block
+    # length: the chunk-64 kernels one by one (f32-state chain, 16-bit chunk_scan)
+    Y64, f64 = forward_by_kernels(X, A, B, C, 64)
     Yi, fi = S.ssd_forward(X, A, B, C, 256, initial_states=S0, return_final_states=True)
     Y0, f0 = S.ssd_forward(torch.zeros_like(X), A, B, C, 256, initial_states=S0, return_final_states=True)
     torch.cuda.synchronize()

@@ -272,7 +272,7 @@ def test_full_r0_layer_span_matches_oracle_with_reference_init():
         y_mod = layer(u)
     torch.cuda.synchronize()
     assert y.shape == (b, L, h * P) and torch.isfinite(y).all() and torch.isfinite(y_mod).all()
-    heads = [0, 1, 17, 40, 63, 64, 100, 127]   # groups 0, 1, 2, 3, 4, 6, 7
+    heads = [0, 1, 17, 40, 63, 64, 90, 100, 127]   # groups 0, 0, 1, 2, 3, 4, 5, 6, 7
     bs = torch.tensor([0, 7])
     cpu = lambda t: t[bs].cpu()  # noqa: E731
     ref = _span_oracle(cpu(x), cpu(z), cpu(Bv), cpu(Cv), cpu(dt), layer, heads, 64)

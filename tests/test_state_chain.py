@@ -234,13 +234,25 @@ def test_chain_f16s_entry_point(b, L, h, N, g, Q, with_dt, with_init, dtype):
     assert torch.equal(_f16_halves(S_in), _f16_halves(S_ref))
 
 
+# 16-bit shapes that ssd_forward runs at their own chunk: F32_SHAPES[:4] with
+# seqlens that 256 does not divide (16-bit inputs at chunk 64 / 128 with
+# seqlen % 256 == 0 run at chunk 256: test_routed_forward_is_the_chunk_256_forward)
+B16_FORWARD_SHAPES = [
+    (2, 2112, 24, 128, 1, 64),
+    (8, 640, 64, 64, 8, 128),
+    (3, 128, 20, 64, 4, 128),
+    (2, 640, 6, 128, 3, 64),
+]
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("b,L,h,N,g,Q", F32_SHAPES[:4])
+@pytest.mark.parametrize("b,L,h,N,g,Q", B16_FORWARD_SHAPES)
 def test_16bit_forward_f16s_equals_kernels_one_by_one(b, L, h, N, g, Q, dtype):
     """ssd_forward on 16-bit inputs at chunk 64 / 128 hands S_in to the 16-bit
     chunk_scan as "f16s": Y and the final state bit for bit against K1, K2 + K3
     (split="f16s") and K4 (split="f16s") through their own entry points."""
     print("CASE 16-bit forward f16s", dtype, b, L, h, N, g, Q, flush=True)
+    assert S.forward_chunk(b, L, h, 64, N, g, Q, dtype) == Q
     X, A, B, C, dt, init = case(dtype, b, L, h, 64, N, g, seed=5 * L + h)
     Y, final = S.ssd_forward(X, A, B, C, Q, dt=dt, initial_states=init, return_final_states=True)
     Acs, decay = S.chunk_cumsum(A, Q)
@@ -249,3 +261,22 @@ def test_16bit_forward_f16s_equals_kernels_one_by_one(b, L, h, N, g, Q, dtype):
     torch.cuda.synchronize()
     assert torch.equal(final, fk)
     assert torch.equal(Y, Yk)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("b,L,h,N,g,Q", [(2, 2048, 24, 128, 1, 64), (8, 512, 64, 64, 4, 128),
+                                         (1, 1024, 32, 128, 8, 64)])
+def test_routed_forward_is_the_chunk_256_forward(b, L, h, N, g, Q, dtype):
+    """16-bit inputs at chunk 64 / 128 with seqlen % 256 == 0 and d_state
+    64 / 128: ssd_forward runs them at chunk 256 (the library's
+    ssd_forward_chunk), so Y and the final state are those of the chunk-256
+    call bit for bit; the no-alloc entry point runs them the same way."""
+    print("CASE routed forward", dtype, b, L, h, N, g, Q, flush=True)
+    assert S.forward_chunk(b, L, h, 64, N, g, Q, dtype) == 256
+    X, A, B, C, dt, init = case(dtype, b, L, h, 64, N, g, seed=7 * L + h)
+    Y, final = S.ssd_forward(X, A, B, C, Q, dt=dt, initial_states=init, return_final_states=True)
+    Y256, f256 = S.ssd_forward(X, A, B, C, 256, dt=dt, initial_states=init, return_final_states=True)
+    Yn, fn = S.ssd_forward_noalloc(X, A, B, C, Q, dt=dt, initial_states=init, return_final_states=True)
+    torch.cuda.synchronize()
+    assert torch.equal(Y, Y256) and torch.equal(final, f256)
+    assert torch.equal(Yn, Y256) and torch.equal(fn, f256)

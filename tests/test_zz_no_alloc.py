@@ -15,6 +15,8 @@ its scale; every other batch element bit for bit (the per-chain forms as
 tests/state_plans.py restates them)."""
 
 import ctypes
+import os
+import re
 
 import pytest
 import torch
@@ -27,7 +29,17 @@ from workloadsuite_amd.configs import CONFIGS, make_inputs
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda"
-SCRATCH = 256 << 20
+
+
+def header_scratch_bytes():
+    """SSD_NOALLOC_SCRATCH_BYTES as include/ssd.h defines it ((size_t)A << B)."""
+    text = open(os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "ssd.h")).read()
+    m = re.search(r"#define SSD_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", text)
+    assert m, "SSD_NOALLOC_SCRATCH_BYTES not found in include/ssd.h"
+    return int(m.group(1)) << int(m.group(2))
+
+
+SCRATCH = header_scratch_bytes()
 
 
 def run_both(cfg, seed, use_dt=False):

@@ -15,11 +15,11 @@ import torch  # noqa: F401  -- must precede the CDLL, see module docstring
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libssd.so")
 
-SSD_ABI_VERSION = 7
+SSD_ABI_VERSION = 8
 DTYPE_F32, DTYPE_BF16, DTYPE_F16 = 0, 1, 2
 STATE_SPLIT_BF16, STATE_SPLIT_F16 = 3, 4  # f32 states as 16-bit (hi, lo) pairs
 STATE_F16S = 5  # f32 states as f16 rows with a power-of-two scale per row
-STATE_F16S_LOCAL = 6  # local states as f16 rows, the row's scale in slot N / 2 of the row
+STATE_F16S_LOCAL = 6  # local states as f16 rows, a scale per row and 16-column tile packed into the item's first rows
 
 # Every symbol include/ssd.h declares.
 EXPORTS = (
@@ -34,6 +34,7 @@ EXPORTS = (
     "ssd_state_passing",
     "ssd_chunk_state_passing",
     "ssd_chunk_scan",
+    "ssd_forward_chunk",
     "ssd_forward",
     "ssd_decode_step",
     "ssd_layer_prep",
@@ -78,6 +79,7 @@ _SIGNATURES = {
                                        _vp, _int, _vp, _vp, _vp]),
     "ssd_chunk_scan": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                               _vp, _vp, _int, _vp, _vp, _i64p, _vp, _epi_p, _vp]),
+    "ssd_forward_chunk": (ctypes.c_int64, [_dims_p, _int, _int]),
     "ssd_forward": (_int, [_dims_p, _int, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _i64p,
                            _vp, _vp, _i64p, _vp, _vp, ctypes.c_size_t, _int, _vp]),
     "ssd_decode_step": (_int, [_dims_p, _int, _vp, _vp, _i64p, _vp, _i64p, _vp, _i64p, _vp, _vp, _i64p,

@@ -1,6 +1,7 @@
 // C ABI of libssd (declared in include/ssd.h): host-side validation and
-// dispatch to the four kernels.  Nothing here allocates, synchronises or keeps
-// state between calls; every kernel goes to the caller's stream.
+// dispatch to the four kernels.  Nothing here allocates or synchronises, and
+// nothing is kept between calls but a per-device cache of the CU count; every
+// kernel goes to the caller's stream.
 #include <hip/hip_runtime.h>
 
 #include <atomic>
@@ -416,6 +417,27 @@ ssd_dims layer_core_dims(const ssd_dims* d, int dtype) {
   return e;
 }
 
+// The chunk length ssd_forward runs at (dims already validated).  As for the
+// layer, MR's block_len only has to divide L.  16-bit inputs with f32 states
+// (handed to chunk_scan as f16 rows), L % 256 == 0 and dstate 64 / 128 run a
+// chunk of 64 or 128 at 256: the persistent kernels, with a quarter of the
+// per-chunk states.  Not when that workspace would be the larger one (many
+// groups: chunk_prep's per-group operands then outgrow the states saved), so
+// a workspace sized by ssd_workspace_bytes for the caller's chunk always
+// suffices.  The SPLIT / bf16 state formats keep the caller's chunk.
+ssd_dims forward_dims(const ssd_dims* d, int dtype, int state_dtype) {
+  ssd_dims e = *d;
+  const bool b16 = dtype == SSD_DTYPE_BF16 || dtype == SSD_DTYPE_F16;
+  const bool f32_states = state_dtype == SSD_DTYPE_F32 || state_dtype == SSD_STATE_F16S;
+  if (b16 && f32_states && (d->chunk == 64 || d->chunk == 128) && d->seqlen % 256 == 0 &&
+      (d->dstate == 64 || d->dstate == 128)) {
+    ssd_dims c = *d;
+    c.chunk = 256;
+    if (ws_layout(&c, SSD_DTYPE_F32).total <= ws_layout(d, SSD_DTYPE_F32).total) e = c;
+  }
+  return e;
+}
+
 struct LayerWs {
   size_t xo, dto, core, total;
   WsLayout cw;
@@ -565,6 +587,11 @@ size_t ssd_workspace_bytes(const ssd_dims* d, int state_dtype) {
   return ws_layout(d, state_dtype).total;
 }
 
+int64_t ssd_forward_chunk(const ssd_dims* d, int dtype, int state_dtype) {
+  if (check_dims_impl(d, dtype) != SSD_OK) return 0;
+  return forward_dims(d, dtype, state_dtype).chunk;
+}
+
 int ssd_chunk_cumsum(const ssd_dims* d, const float* a, const int64_t a_strides[3],
                      float* a_cumsum, float* chunk_decay, void* stream) {
   int rc = check_dims_impl(d, SSD_DTYPE_F32);
@@ -606,7 +633,8 @@ int ssd_chunk_state(const ssd_dims* d, int dtype, const void* x, const int64_t x
   if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
   if (!a_cumsum || !states) return SSD_ERR_NULL_POINTER;
-  if (!aligned16(states)) return SSD_ERR_MISALIGNED;
+  // the kernels copy a_cumsum to LDS 16 bytes at a time
+  if (!aligned16(states) || !aligned16(a_cumsum)) return SSD_ERR_MISALIGNED;
   if (prep && (reinterpret_cast<uintptr_t>(prep) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
   ChunkStateArgs p = make_state_args(d, x, x_strides, bmat, b_strides, dt, dt_strides, a_cumsum, states);
   // f16 local states: the chunk-256 kernel for 16-bit inputs only
@@ -654,7 +682,7 @@ int ssd_chunk_state_passing(const ssd_dims* d, int dtype, const void* x, const i
   if ((rc = check_vec_operand(bmat, b_strides, 4, dtype))) return rc;
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
   if (!a_cumsum || !chunk_decay || !states || (f16s && !state_scales)) return SSD_ERR_NULL_POINTER;
-  if (!aligned16(states) || (initial_states && !aligned16(initial_states)) ||
+  if (!aligned16(states) || !aligned16(a_cumsum) || (initial_states && !aligned16(initial_states)) ||
       (final_states && !aligned16(final_states)) || (f16s && (reinterpret_cast<uintptr_t>(state_scales) & 3u)))
     return SSD_ERR_MISALIGNED;
   if (prep && (reinterpret_cast<uintptr_t>(prep) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
@@ -685,6 +713,8 @@ int ssd_chunk_scan(const ssd_dims* d, int dtype, const void* x, const int64_t x_
   if ((rc = check_vec_operand(cmat, c_strides, 4, dtype))) return rc;
   if (dt && (rc = check_scalar_operand(dt, dt_strides, 3))) return rc;
   if (!a_cumsum || !states || (f16s && !state_scales)) return SSD_ERR_NULL_POINTER;
+  // a_cumsum and the states are copied to LDS 16 bytes at a time
+  if (!aligned16(a_cumsum) || !aligned16(states)) return SSD_ERR_MISALIGNED;
   if (f16s && (reinterpret_cast<uintptr_t>(state_scales) & 3u)) return SSD_ERR_MISALIGNED;
   if ((rc = check_output(y, y_strides, dtype))) return rc;
   if ((rc = check_epilogue(epilogue, dtype))) return rc;
@@ -721,6 +751,9 @@ int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_str
     return SSD_ERR_UNSUPPORTED_DTYPE;
   if (!workspace) return SSD_ERR_NULL_POINTER;
   if ((reinterpret_cast<uintptr_t>(workspace) % kWsAlign) != 0) return SSD_ERR_MISALIGNED;
+  // the chunk the forward runs at (never a larger workspace than d's own)
+  const ssd_dims e = forward_dims(d, dtype, state_dtype);
+  d = &e;
   const WsLayout w = ws_layout(d, f32_layout(state_dtype) ? SSD_DTYPE_F32 : state_dtype);
   if (workspace_bytes < w.total) return SSD_ERR_WORKSPACE_TOO_SMALL;
   // Validate every operand before the first launch, so a bad argument never

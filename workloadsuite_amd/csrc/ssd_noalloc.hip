@@ -12,6 +12,10 @@
 // device address comes from hipGetSymbolAddress, taken once per device with
 // that device current and cached here.
 //
+// The array lives in the code object's data segment: it is reserved on every
+// device where libssd's code object loads, from then until the process ends,
+// whether or not this entry point is ever called.
+//
 // When one call's workspace does not fit, the batch is processed in slices
 // whose workspace does; a shape whose single batch element needs more than
 // kScratchBytes is rejected (SSD_ERR_WORKSPACE_TOO_SMALL) before anything is
@@ -77,6 +81,12 @@ extern "C" int ssd_forward_noalloc(const ssd_dims* d, int dtype, const void* x, 
   if (!x || !x_strides || !a || !a_strides || !bmat || !b_strides || !cmat || !c_strides || !y || !y_strides ||
       (dt && !dt_strides))
     return SSD_ERR_NULL_POINTER;
+  // the chunk ssd_forward runs at (the routing depends on the shape's ratios,
+  // not on the batch; every slice below is run at it explicitly)
+  ssd_dims e = *d;
+  e.chunk = ssd_forward_chunk(d, dtype, state_dtype);
+  if (e.chunk == 0) return SSD_ERR_UNSUPPORTED_DTYPE;
+  d = &e;
   const size_t need = ssd_workspace_bytes(d, state_dtype);
   if (need == 0) return SSD_ERR_UNSUPPORTED_DTYPE;
   // the largest batch slice whose workspace fits

@@ -318,20 +318,24 @@ hipError_t launch_state_passing(const StatePassingArgs& a, int state_dtype, hipS
   if (a.bh_begin < 0 || a.bh_count < 0 || a.bh_begin + (int64_t)a.bh_count > all) return hipErrorInvalidValue;
   const int64_t chains = a.bh_count > 0 ? a.bh_count : all - a.bh_begin;
   if (a.f16s) {
-    // 4 states per thread and batches of 4 chunks: 75 VGPRs, so the 80 chains
-    // of C4 fit the device in one wave of workgroups (8 states per thread and
-    // batches of 8: 196 VGPRs, 0.53 instead of 0.58 of HBM peak at C4)
-    constexpr int spt = 4;
+    // 8 states per thread (two 16-byte loads of f32 local states or one of f16
+    // ones, one 16-byte f16 store per chunk) in batches of 2 chunks: 76 VGPRs.
+    // Against 4 states per thread in batches of 4 (MI355X, rotated buffers
+    // beyond the Infinity Cache): C3 (f32 local states in) 52.5 -> 51.0 us,
+    // 0.646 of HBM peak, where a hand-written stream at the same 2 : 1 read /
+    // write mix with plain stores reaches 0.633 and with non-temporal ones
+    // 0.670 (bench.py --hbm-probe); C4 (f16 local states in) 164 -> 161 us.
+    constexpr int spt = 8, unroll = 2;
     const bool f16l = state_dtype == SSD_STATE_F16S_LOCAL;
     if ((state_dtype != SSD_DTYPE_F32 && !f16l) || a.split_dtype != 0 || !a.sscale || (PN / spt) % 256 != 0)
       return hipErrorInvalidValue;
     const dim3 grid((unsigned)(chains * ((PN / spt + 255) / 256)));
     if (a.dstate == 128) {
-      if (f16l) state_passing_f16s_kernel<128, spt, 4, true><<<grid, 256, 0, stream>>>(a);
-      else state_passing_f16s_kernel<128, spt, 4, false><<<grid, 256, 0, stream>>>(a);
+      if (f16l) state_passing_f16s_kernel<128, spt, unroll, true><<<grid, 256, 0, stream>>>(a);
+      else state_passing_f16s_kernel<128, spt, unroll, false><<<grid, 256, 0, stream>>>(a);
     } else if (a.dstate == 64) {
-      if (f16l) state_passing_f16s_kernel<64, spt, 4, true><<<grid, 256, 0, stream>>>(a);
-      else state_passing_f16s_kernel<64, spt, 4, false><<<grid, 256, 0, stream>>>(a);
+      if (f16l) state_passing_f16s_kernel<64, spt, unroll, true><<<grid, 256, 0, stream>>>(a);
+      else state_passing_f16s_kernel<64, spt, unroll, false><<<grid, 256, 0, stream>>>(a);
     } else {
       return hipErrorInvalidValue;
     }

@@ -36,6 +36,7 @@ from . import _lib
 
 __all__ = [
     "ssd_forward",
+    "forward_chunk",
     "ssd_forward_noalloc",
     "ssd_core",
     "chunk_cumsum",
@@ -226,17 +227,50 @@ def workspace_bytes(batch, seqlen, nheads, headdim, dstate, ngroups, chunk_size,
     return n
 
 
+def forward_chunk(batch, seqlen, nheads, headdim, dstate, ngroups, chunk_size, dtype,
+                  state_dtype=torch.float32, state_format=None) -> int:
+    """The chunk length ``ssd_forward`` runs these dims at (the library's
+    ``ssd_forward_chunk``): ``chunk_size``, or 256 for 16-bit inputs with
+    float32 states, seqlen % 256 == 0 and d_state 64 / 128 where that
+    workspace is not the larger one."""
+    d = _lib.dims(batch, seqlen, nheads, headdim, dstate, ngroups, chunk_size)
+    q = _lib.load().ssd_forward_chunk(ctypes.byref(d), _DTYPES[dtype], _handover(state_format, dtype, state_dtype))
+    if q == 0:
+        _lib.check(_lib.load().ssd_check_dims(ctypes.byref(d), _DTYPES[dtype]))
+    return q
+
+
 def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
                 return_final_states=False, state_dtype=torch.float32, state_format=None):
     """Chunked SSD forward (MR:123-162) on the HIP device.
 
     Returns Y, or (Y, final_states) with ``return_final_states``.
-    ``state_dtype`` is the storage type of the per-chunk states between the
-    kernels (float32, or bfloat16 for 16-bit inputs); the recurrence itself
-    always runs in float32.  ``state_format`` (float32 states, 16-bit inputs):
-    how chunk_scan receives them -- None (library default: f16 rows with a
-    power-of-two scale per row where the chunk-256 kernels run), "split"
-    (hi/lo pairs of the inputs' type) or "f16s".
+
+    ``chunk_size`` is MR's block_len and only has to divide the seqlen: every
+    chunking evaluates the same linear recurrence (MR:152-161).  For 16-bit
+    inputs with float32 states, seqlen % 256 == 0 and d_state 64 / 128 the
+    library runs chunk 64 / 128 at 256 (``forward_chunk``), which changes
+    rounding only.
+
+    ``state_dtype`` is the storage type of the per-chunk states (float32, or
+    bfloat16 for 16-bit inputs); the recurrence itself always runs in
+    float32.  ``state_format`` (float32 states, 16-bit inputs): how the states
+    entering each chunk reach chunk_scan --
+
+    * None (the default): f16 rows with a power-of-two scale per row
+      ("f16s") wherever a 16-bit chunk_scan reads them: chunk 256 with
+      d_state 64 / 128, and chunk 64 / 128 with chunk x d_state <= 8192.
+      Where chunk_state and state_passing then run as two launches (chunk 256
+      outside the one-launch state chain, and the chain's segments) the local
+      states between them cross HBM as f16 rows with a scale per row and
+      16-column tile (SSD_STATE_F16S_LOCAL); the state chain keeps them in
+      float32 registers.  Which launches run depends on batch x heads and the
+      device's CU count, so the last bits of Y and of the final state are not
+      invariant to the batch size (within the 16-bit tolerance, and the final
+      state within ~1e-3 of its scale).
+    * "split": hi/lo pairs of the inputs' type at chunk 256 (plain float32
+      at chunk 64 / 128); every local state stays float32.
+    * "f16s": as the default.
     """
     b, L, h, P, g, N = _shape_check(X, A, B, C, chunk_size, dt, initial_states)
     dev = _device_check(X, A, B, C, dt, initial_states)
@@ -251,7 +285,9 @@ def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
     Y = torch.empty((b, L, h, P), dtype=X.dtype, device=dev)
     final = torch.empty((b, h, P, N), dtype=torch.float32, device=dev) if return_final_states else None
     sd = _handover(state_format, X.dtype, state_dtype)
-    ws_n = lib.ssd_workspace_bytes(ctypes.byref(d), sd)
+    # the workspace of the chunk the library runs at
+    dw = _lib.dims(b, L, h, P, N, g, lib.ssd_forward_chunk(ctypes.byref(d), _DTYPES[X.dtype], sd))
+    ws_n = lib.ssd_workspace_bytes(ctypes.byref(dw), sd)
     ws = torch.empty(ws_n, dtype=torch.uint8, device=dev)
     rc = lib.ssd_forward(ctypes.byref(d), _DTYPES[X.dtype],
                          _ptr(X), _lib.strides(X), _ptr(A), _lib.strides(A),
