@@ -106,6 +106,14 @@ def kernel_model(cfg, state_dtype, handover=None, local_f16=False, cb_in_scan=Tr
     }
 
 
+def takes_small_path(cfg, state_dtype):
+    """ssd_forward's one-launch path for small states and short chains
+    (ssd_small_supported in the library): f32 states, d_state 16 / 32,
+    chunk 64 / 128, at most 16 chunks per chain."""
+    return (state_dtype == torch.float32 and cfg.dstate in (16, 32) and cfg.chunk in (64, 128)
+            and cfg.nchunks <= 16)
+
+
 def small_chunk_shape(cfg):
     """chunk 64 / 128, d_state 64 / 128, chunk x d_state <= 8192: the shapes of
     the f32-state chain and of the 16-bit chunk_scan for f32 states."""
@@ -494,8 +502,18 @@ def main():
     }
     if prep is None:
         del kfn["chunk_prep"]
+    small = takes_small_path(kcfg, state_dtype)
+    if small:
+        # the forward is one launch (ssd_small): time it, with the forward's
+        # minimum bytes and flops; the four stages' entry points are not what
+        # it runs
+        kfn = {"ssd_small": lambda: S.ssd_forward(X, A, B, C, cfg.chunk, initial_states=init,
+                                                  return_final_states=cfg.final_state, state_dtype=state_dtype,
+                                                  state_format=args.state_format)}
     model = kernel_model(kcfg, state_dtype, split if isinstance(split, str) else None, local_f16,
                          cb_in_scan=prep is None)
+    f_min, b_min = end_to_end_model(cfg)
+    model["ssd_small"] = dict(bytes=b_min, flops=f_min)
     kernels = {}
     pre_launches = 0
     for name, fn in kfn.items():
@@ -569,7 +587,6 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     tokens_per_s = cfg.tokens * args.steps / wall
 
-    f_min, b_min = end_to_end_model(cfg)
     roof_tps = min(PEAK_TFLOPS[cfg.dtype] * 1e12 / (f_min / cfg.tokens), PEAK_HBM_GBS * 1e9 / (b_min / cfg.tokens))
 
     out = {
@@ -590,7 +607,7 @@ def main():
                    "dstate": cfg.dstate, "chunk": cfg.chunk, "chunk_run": run_chunk, "ngroups": cfg.ngroups,
                    "inputs": f"{DTYPE_NAMES[cfg.dtype]} X/B/C, f32 A", "state_storage": args.state_dtype,
                    "state_handover": split if isinstance(split, str) else ("split" if split is not None else None),
-                   "local_states": ("f16 rows" if local_f16 else
+                   "local_states": ("in LDS (one-launch forward)" if small else "f16 rows" if local_f16 else
                                     "in registers (state chain)" if takes_state_chain(kcfg, split, state_dtype)
                                     else args.state_dtype),
                    "final_state": cfg.final_state, "initial_state": cfg.init_state},

@@ -143,7 +143,9 @@ int ssd_check_dims(const ssd_dims* d, int dtype);
  * states at the shapes where a 16-bit chunk_scan reads F16S (chunk 256, or
  * chunk 64 / 128 with chunk x dstate <= 8192; dstate 64 / 128) their row
  * scales [b, c, h, P] f32, and ssd_chunk_prep_bytes(d), each region 256-byte
- * aligned.  0 when dims are invalid. */
+ * aligned.  256 where ssd_forward runs the whole forward as one launch and
+ * uses no workspace (f32 states, dstate 16 / 32, chunk 64 / 128 with chunk x
+ * dstate <= 2048, at most 16 chunks).  0 when dims are invalid. */
 size_t ssd_workspace_bytes(const ssd_dims* d, int state_dtype);
 
 /* K1 -- intra-chunk cumsum of the log-decays and the per-chunk total decay.

@@ -325,3 +325,23 @@ def test_forward_chunk_keeps_the_chunk_where_chunk_prep_outweighs_the_states_sav
     move = _lib.SSDDims(8, 512, 64, 64, 64, 4, 128)
     assert lib.ssd_forward_chunk(ctypes.byref(keep), _lib.DTYPE_BF16, 0) == 128
     assert lib.ssd_forward_chunk(ctypes.byref(move), _lib.DTYPE_BF16, 0) == 256
+
+
+def test_one_launch_forward_needs_no_workspace():
+    """d_state 16 / 32 at chunk 64 / 128 (chunk x d_state <= 2048) with at most
+    16 chunks and f32 states: ssd_forward runs as one launch and uses no
+    workspace, so ssd_workspace_bytes reports 256; bf16 states, 17 chunks or
+    chunk 128 x d_state 32 keep the four-kernel workspace."""
+    lib = _lib.load()
+    def ws(sd=_lib.DTYPE_F32, **kw):
+        dims = dict(batch=16, seqlen=128, nheads=8, headdim=64, dstate=16, ngroups=8, chunk=64)
+        dims.update(kw)
+        return lib.ssd_workspace_bytes(ctypes.byref(_lib.SSDDims(*[dims[k] for k in (
+            "batch", "seqlen", "nheads", "headdim", "dstate", "ngroups", "chunk")])), sd)
+
+    assert ws() == 256                                   # C1
+    assert ws(dstate=32) == 256 and ws(chunk=128, seqlen=256) == 256
+    assert ws(seqlen=64 * 16) == 256 and ws(seqlen=64 * 17) > 256
+    assert ws(_lib.DTYPE_BF16) > 256
+    assert ws(dstate=32, chunk=128, seqlen=256) > 256
+    assert ws(dstate=64) > 256

@@ -729,3 +729,92 @@ def test_state_passing_addresses(name):
             c0 = np.arange(0, nchunks + 2 * unroll, unroll)
             c = np.minimum(c0[:, None] + np.arange(unroll)[None, :], nchunks - 1)
             inside("chain chunk", c, 0, nchunks)
+
+
+# ---------------------------------------------------------------------------
+# the one-launch forward for small states (ssd_small.hip)
+# ---------------------------------------------------------------------------
+
+@pytest.mark.parametrize("es", [4, 2])
+@pytest.mark.parametrize("Q,N", [(64, 16), (64, 32), (128, 16)])
+@pytest.mark.parametrize("PS", [1, 2])
+def test_small_forward_addresses(Q, N, PS, es):
+    """Every LDS index of each phase inside its array, every global column
+    inside the workgroup's p range (two workgroups per chain take halves of
+    p), and each workgroup's y, state and final-state writes a partition of
+    its part; C1's shape and the other supported (chunk, d_state) pairs, f32
+    and 16-bit inputs."""
+    pin("ssd_small.hip",
+        "constexpr int PP = kP / PS;",
+        "constexpr int QT = PP / 16;",
+        "constexpr int XPR = PP / VPP;",
+        "constexpr int XPT = Q * XPR / kT;",
+        "constexpr int BPT = (Q * BPR + kT - 1) / kT;",
+        "const int bh = blockIdx.x / PS, pc0 = PP * (blockIdx.x % PS);",
+        "const int e = t + kT * k, r = e / XPR, q = e % XPR;",
+        "xr[k] = *reinterpret_cast<const u32x4*>(xg + (l0 + r) * p.sxl + VPP * q);",
+        "for (int j = 0; j < VPP; ++j) xt[VPP * q + j][r] = v[j];",
+        "acc = mfma4(ld4(&cs[16 * r + i][16 * nb + 4 * g]), ld4(&bs[16 * cc + i][16 * nb + 4 * g]), acc);",
+        "wl[l][s] = s <= l ? acc[jj] * exp2f(acl[l] - as) * ds : 0.f;",
+        "constexpr int QPW = R == 4 ? QT / 2 : QT;",
+        "const int r = half ? R - 1 - wave : wave;",
+        "const int q0 = R == 4 ? QPW * half : 0;",
+        "for (int sb = 0; sb <= r; ++sb) {",
+        "yrow[16 * (q0 + qq) + i] = from_f32<T>(",
+        "const int tile = wave + 4 * k, q = tile % QT, m = tile / QT;",
+        "acc = mfma4(ld4(&xt[16 * q + i][16 * lb + 4 * g]), ld4(&bwt[16 * m + i][16 * lb + 4 * g]), acc);",
+        "p.final_state[(int64_t)bh * kP * N + (int64_t)(pc0 + pp) * N + n] = snew[k][jj];",
+        "ss[pp][n] = init ? p.init[(int64_t)bh * kP * N + (int64_t)pc0 * N + e] : 0.f;")
+    P, T = 64, 256
+    PP, VPP = P // PS, 16 // es
+    QT, XPR, BPR = PP // 16, PP // VPP, N // VPP
+    XPT, BPT = Q * XPR // T, -(-(Q * BPR) // T)
+    R, QS, NS, NT = Q // 16, Q + 4, N + 4, N // 16
+    assert XPT * T == Q * XPR
+    lds_bytes = 4 * (PP * QS + 2 * Q * NS + N * QS + Q * QS + PP * NS + 4 * Q)
+    assert lds_bytes <= 160 * 1024
+    t = np.arange(T)
+    lane, wave = t % 64, t // 64
+    g, i = lane // 16, lane % 16
+    # x pieces: rows and global columns (pc0 + ...) of this workgroup
+    e = (t[None, :] + T * np.arange(XPT)[:, None]).ravel()
+    r, q = e // XPR, e % XPR
+    inside("x rows", r, 0, Q)
+    inside("x columns of the part", VPP * q + VPP - 1, 0, PP)
+    eb = (t[None, :] + T * np.arange(BPT)[:, None]).ravel()
+    eb = eb[eb < Q * BPR]
+    inside("B / C rows", eb // BPR, 0, Q)
+    inside("B / C columns", VPP * (eb % BPR) + VPP - 1, 0, N)
+    # W tiles (causal), y tiles, state tiles
+    taus = np.arange(R * (R + 1) // 2)
+    rr = np.array([max(k for k in range(R) if k * (k + 1) // 2 <= tau) for tau in taus])
+    cc = taus - rr * (rr + 1) // 2
+    assert (cc <= rr).all() and len(set(zip(rr, cc))) == len(taus)
+    QPW = QT // 2 if R == 4 else QT
+    covered = np.zeros((Q, PP), np.int64)
+    for w in range(4):
+        for half in range(2):
+            row_t = R - 1 - w if half else w
+            q0 = QPW * half if R == 4 else 0
+            for qq in range(QPW):
+                col = 16 * (q0 + qq) + np.arange(16)
+                inside("y p tiles", col, 0, PP)
+                for gg in range(4):
+                    for jj in range(4):
+                        covered[16 * row_t + 4 * gg + jj, col] += 1
+    assert (covered == 1).all(), "every y element of the part written once"
+    TS = QT * NT
+    st = np.zeros((PP, N), np.int64)
+    for w in range(4):
+        for k in range(-(-TS // 4)):
+            tile = w + 4 * k
+            if tile < TS:
+                qt, m = tile % QT, tile // QT
+                for gg in range(4):
+                    for jj in range(4):
+                        st[16 * qt + 4 * gg + jj, 16 * m + np.arange(16)] += 1
+    assert (st == 1).all(), "every state element of the part written once"
+    # init / final: the part's rows of the [P, N] state
+    ei = np.arange(PP * N)
+    for pc0 in range(0, P, PP):
+        inside("state element", pc0 * N + ei, 0, P * N)

@@ -37,6 +37,7 @@ SOURCES = [
     "ssd_layer_prep.hip",
     "ssd_decode.hip",
     "ssd_noalloc.hip",
+    "ssd_small.hip",
 ]
 
 # The streaming probe behind bench.py --hbm-probe: its own library, outside

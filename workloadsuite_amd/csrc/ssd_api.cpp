@@ -438,6 +438,13 @@ ssd_dims forward_dims(const ssd_dims* d, int dtype, int state_dtype) {
   return e;
 }
 
+// ssd_forward's one-launch path for small states and short chains (f32
+// states; the shapes ssd_small_supported takes)
+bool small_forward(const ssd_dims* d, int state_dtype) {
+  return state_dtype == SSD_DTYPE_F32 &&
+         ssd::ssd_small_supported(d->batch, d->nheads, d->headdim, d->dstate, d->chunk, d->seqlen / d->chunk);
+}
+
 struct LayerWs {
   size_t xo, dto, core, total;
   WsLayout cw;
@@ -582,6 +589,8 @@ int ssd_check_dims(const ssd_dims* d, int dtype) { return check_dims_impl(d, dty
 
 size_t ssd_workspace_bytes(const ssd_dims* d, int state_dtype) {
   if (check_dims_impl(d, SSD_DTYPE_BF16) != SSD_OK) return 0;
+  // the one-launch forward of small states uses no workspace
+  if (small_forward(d, state_dtype)) return kWsAlign;
   if (f32_layout(state_dtype)) state_dtype = SSD_DTYPE_F32;
   if (state_dtype != SSD_DTYPE_F32 && state_dtype != SSD_DTYPE_BF16) return 0;
   return ws_layout(d, state_dtype).total;
@@ -754,8 +763,9 @@ int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_str
   // the chunk the forward runs at (never a larger workspace than d's own)
   const ssd_dims e = forward_dims(d, dtype, state_dtype);
   d = &e;
+  const bool small = small_forward(d, state_dtype);
   const WsLayout w = ws_layout(d, f32_layout(state_dtype) ? SSD_DTYPE_F32 : state_dtype);
-  if (workspace_bytes < w.total) return SSD_ERR_WORKSPACE_TOO_SMALL;
+  if (workspace_bytes < (small ? kWsAlign : w.total)) return SSD_ERR_WORKSPACE_TOO_SMALL;
   // Validate every operand before the first launch, so a bad argument never
   // leaves a partially computed result behind.
   if ((rc = check_scalar_operand(a, a_strides, 3))) return rc;
@@ -766,6 +776,45 @@ int ssd_forward(const ssd_dims* d, int dtype, const void* x, const int64_t x_str
   if ((rc = check_output(y, y_strides, dtype))) return rc;
   if ((initial_states && !aligned16(initial_states)) || (final_states && !aligned16(final_states)))
     return SSD_ERR_MISALIGNED;
+
+  // small states and short chains: the whole forward in one launch, the
+  // states kept in f32 (the workspace is not used)
+  if (small) {
+    ssd::SmallArgs sm;
+    sm.x = x;
+    sm.sxb = x_strides[0];
+    sm.sxl = x_strides[1];
+    sm.sxh = x_strides[2];
+    sm.a = a;
+    sm.sab = a_strides[0];
+    sm.sal = a_strides[1];
+    sm.sah = a_strides[2];
+    sm.bm = bmat;
+    sm.sbb = b_strides[0];
+    sm.sbl = b_strides[1];
+    sm.sbg = b_strides[2];
+    sm.cm = cmat;
+    sm.scb = c_strides[0];
+    sm.scl = c_strides[1];
+    sm.scg = c_strides[2];
+    sm.dt = dt;
+    sm.sdb = dt ? dt_strides[0] : 0;
+    sm.sdl = dt ? dt_strides[1] : 0;
+    sm.sdh = dt ? dt_strides[2] : 0;
+    sm.init = initial_states;
+    sm.final_state = final_states;
+    sm.y = y;
+    sm.syb = y_strides[0];
+    sm.syl = y_strides[1];
+    sm.syh = y_strides[2];
+    sm.batch = (int)d->batch;
+    sm.nchunks = (int)(d->seqlen / d->chunk);
+    sm.nheads = (int)d->nheads;
+    sm.ngroups = (int)d->ngroups;
+    sm.dstate = (int)d->dstate;
+    sm.chunk = (int)d->chunk;
+    return hip_status(ssd::launch_ssd_small(sm, dtype, (hipStream_t)stream));
+  }
 
   char* ws = static_cast<char*>(workspace);
   const CumsumArgs k1 = make_cumsum_args(d, a, a_strides, reinterpret_cast<float*>(ws + w.acs),

@@ -214,4 +214,28 @@ hipError_t launch_chunk_scan_f32(const ChunkScanArgs& a, hipStream_t stream);
 bool chunk_scan_b16_supported(const ChunkScanArgs& a, int dtype, int state_dtype);
 hipError_t launch_chunk_scan_b16(const ChunkScanArgs& a, int dtype, hipStream_t stream);
 
+// The whole forward in one launch for small states and short chains
+// (ssd_small.hip): d_state 16 / 32, chunk 64 / 128, at most kSmallMaxChunks
+// chunks per chain, f32 states kept in LDS; one workgroup per (b, h) chain.
+constexpr int64_t kSmallMaxChunks = 16;
+struct SmallArgs {
+  const void* x;
+  int64_t sxb, sxl, sxh;  // x [b, L, h, P], unit stride over P
+  const float* a;
+  int64_t sab, sal, sah;  // A (log-decay A dt) [b, L, h]
+  const void* bm;
+  int64_t sbb, sbl, sbg;  // bmat [b, L, g, N]
+  const void* cm;
+  int64_t scb, scl, scg;  // cmat [b, L, g, N]
+  const float* dt;        // optional [b, L, h]
+  int64_t sdb, sdl, sdh;
+  const float* init;      // optional [b, h, P, N]
+  float* final_state;     // optional [b, h, P, N]
+  void* y;
+  int64_t syb, syl, syh;  // y [b, L, h, P], unit stride over P
+  int batch, nchunks, nheads, ngroups, dstate, chunk;
+};
+bool ssd_small_supported(int64_t batch, int64_t nheads, int64_t headdim, int64_t dstate, int64_t chunk, int64_t nchunks);
+hipError_t launch_ssd_small(const SmallArgs& a, int dtype, hipStream_t stream);
+
 }  // namespace ssd

@@ -167,6 +167,15 @@ def _stream(dev):
     return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
 
 
+# torch's current stream of a device as a raw handle, without building a
+# Stream object (the accessor torch's own generated code uses), where present
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
+def _stream_fast(dev):
+    return _raw_stream(dev.index) if _raw_stream is not None else _stream(dev)
+
+
 def _shape_check(X, A, B, C, chunk_size, dt, initial_states):
     if X.dim() != 4:
         raise ValueError(f"X must be [batch, seqlen, nheads, headdim], got {tuple(X.shape)}")
@@ -240,6 +249,48 @@ def forward_chunk(batch, seqlen, nheads, headdim, dstate, ngroups, chunk_size, d
     return q
 
 
+# ssd_forward's per-call host work, kept per layout: the ctypes dims and
+# stride arrays, the workspace size and the output shapes, for operands that
+# the kernels take as they are (no copy).  Keyed by every shape, stride,
+# dtype and device the checks depend on; data pointers (16-byte alignment)
+# are checked on every call.
+_PLANS = {}
+_PLANS_MAX = 256
+_NO_WORKSPACE = {}  # device -> a 256-byte buffer for the forwards that use no workspace
+
+
+class _Plan(NamedTuple):
+    dims: object
+    dtype: int
+    sd: int
+    ws_n: int
+    strides: tuple   # X, A, B, C, dt (or None), Y
+    y_shape: tuple
+    f_shape: tuple
+
+
+def _layout_key(t):
+    return None if t is None else (t.shape, t.stride(), t.dtype, t.device)
+
+
+def _unchanged(t, t0):
+    """t is t0's memory as it was (no copy or conversion on the way)."""
+    if t is None or t0 is None:
+        return t is None and t0 is None
+    return t.data_ptr() == t0.data_ptr() and t.dtype == t0.dtype and t.stride() == t0.stride()
+
+
+def _aligned(*ts):
+    return all(t is None or t.data_ptr() % 16 == 0 for t in ts)
+
+
+def _no_workspace(dev):
+    buf = _NO_WORKSPACE.get(dev)
+    if buf is None:
+        buf = _NO_WORKSPACE[dev] = torch.empty(256, dtype=torch.uint8, device=dev)
+    return buf
+
+
 def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
                 return_final_states=False, state_dtype=torch.float32, state_format=None):
     """Chunked SSD forward (MR:123-162) on the HIP device.
@@ -272,10 +323,33 @@ def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
       at chunk 64 / 128); every local state stays float32.
     * "f16s": as the default.
     """
+    key = (_layout_key(X), _layout_key(A), _layout_key(B), _layout_key(C), _layout_key(dt),
+           _layout_key(initial_states), chunk_size, return_final_states, state_dtype, state_format)
+    plan = _PLANS.get(key)
+    if plan is not None and _aligned(X, B, C, initial_states):
+        dev = X.device
+        Y = torch.empty(plan.y_shape, dtype=X.dtype, device=dev)
+        final = torch.empty(plan.f_shape, dtype=torch.float32, device=dev) if return_final_states else None
+        ws = _no_workspace(dev) if plan.ws_n <= 256 else torch.empty(plan.ws_n, dtype=torch.uint8, device=dev)
+        sx, sa, sb, sc, sdt, sy = plan.strides
+        _lib.check(_lib.load().ssd_forward(
+            ctypes.byref(plan.dims), plan.dtype, X.data_ptr(), sx, A.data_ptr(), sa, B.data_ptr(), sb,
+            C.data_ptr(), sc, None if dt is None else dt.data_ptr(), sdt,
+            None if initial_states is None else initial_states.data_ptr(), Y.data_ptr(), sy,
+            None if final is None else final.data_ptr(), ws.data_ptr(), plan.ws_n, plan.sd, _stream_fast(dev)))
+        return (Y, final) if return_final_states else Y
+    out = _ssd_forward(X, A, B, C, chunk_size, dt, initial_states, return_final_states, state_dtype,
+                       state_format, key)
+    return out
+
+
+def _ssd_forward(X, A, B, C, chunk_size, dt, initial_states, return_final_states, state_dtype, state_format, key):
+    """The checks, operand conversions and call of ssd_forward (and its plan for the layout)."""
     b, L, h, P, g, N = _shape_check(X, A, B, C, chunk_size, dt, initial_states)
     dev = _device_check(X, A, B, C, dt, initial_states)
     lib = _lib.load()
     d = _dims(b, L, h, P, N, g, chunk_size)
+    X0, B0, C0, A0, dt0, init0 = X, B, C, A, dt, initial_states
     X = _vec_operand(X.detach())
     Bm = _vec_operand(B.detach())
     Cm = _vec_operand(C.detach())
@@ -288,14 +362,19 @@ def ssd_forward(X, A, B, C, chunk_size, dt=None, initial_states=None,
     # the workspace of the chunk the library runs at
     dw = _lib.dims(b, L, h, P, N, g, lib.ssd_forward_chunk(ctypes.byref(d), _DTYPES[X.dtype], sd))
     ws_n = lib.ssd_workspace_bytes(ctypes.byref(dw), sd)
-    ws = torch.empty(ws_n, dtype=torch.uint8, device=dev)
+    ws = _no_workspace(dev) if ws_n <= 256 else torch.empty(ws_n, dtype=torch.uint8, device=dev)
+    strides = (_lib.strides(X), _lib.strides(A), _lib.strides(Bm), _lib.strides(Cm),
+               _lib.strides(dt) if dt is not None else None, _lib.strides(Y))
     rc = lib.ssd_forward(ctypes.byref(d), _DTYPES[X.dtype],
-                         _ptr(X), _lib.strides(X), _ptr(A), _lib.strides(A),
-                         _ptr(Bm), _lib.strides(Bm), _ptr(Cm), _lib.strides(Cm),
-                         _ptr(dt), _lib.strides(dt) if dt is not None else None,
-                         _ptr(init), _ptr(Y), _lib.strides(Y), _ptr(final),
+                         _ptr(X), strides[0], _ptr(A), strides[1], _ptr(Bm), strides[2], _ptr(Cm), strides[3],
+                         _ptr(dt), strides[4], _ptr(init), _ptr(Y), strides[5], _ptr(final),
                          _ptr(ws), ws_n, sd, _stream(dev))
     _lib.check(rc)
+    # the same layout next time: no checks or conversions, where none were needed
+    as_is = all(_unchanged(t, t0) for t, t0 in ((X, X0), (Bm, B0), (Cm, C0), (A, A0), (dt, dt0), (init, init0)))
+    if as_is and len(_PLANS) < _PLANS_MAX:
+        _PLANS[key] = _Plan(d, _DTYPES[X.dtype], sd, ws_n, strides, tuple(Y.shape),
+                            None if final is None else tuple(final.shape))
     return (Y, final) if return_final_states else Y
 
 
