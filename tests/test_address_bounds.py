@@ -258,6 +258,8 @@ def test_chunk_state_q256_and_chain_addresses(name):
         "const frag8<T>* bnext = btf_of(has_next ? c + 1 : c);",
         "*reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;",
         "sp.sscale[(((int64_t)b * p.nchunks + c) * p.nheads + h) * kP + row] = __builtin_ldexpf(1.f, e);",
+        "bh = xcd_remap((int)blockIdx.x, plan.nfull);",
+        "const int sg = xcd_remap((int)blockIdx.x - plan.nfull, (int)gridDim.x - plan.nfull);",
         "bh = plan.nfull + sg / plan.seg_per_chain;",
         "c0 = (sg % plan.seg_per_chain) * plan.seg_len;",
         "c1 = min(c0 + plan.seg_len, p.nchunks);",
@@ -302,8 +304,9 @@ def test_chunk_state_q256_and_chain_addresses(name):
     grid = nfull + (chains - nfull) * spc
     blocks = np.arange(grid)
     local = blocks >= nfull
-    sg = blocks - nfull
-    bh = np.where(local, nfull + sg // spc, blocks)
+    # whole chains and segments are each dealt out XCD by XCD
+    sg = np.where(local, xcd_remap(np.maximum(blocks - nfull, 0), max(grid - nfull, 1)), 0)
+    bh = np.where(local, nfull + sg // spc, xcd_remap(np.minimum(blocks, nfull - 1), nfull))
     c0 = np.where(local, (sg % spc) * seg_len, 0)
     c1 = np.where(local, np.minimum(c0 + seg_len, nc), nc)
     live = c0 < c1

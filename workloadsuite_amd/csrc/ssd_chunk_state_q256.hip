@@ -362,9 +362,10 @@ hipError_t launch_ts(const ChunkStateArgs& a, hipStream_t stream) {
 // at the start of the step instead costs 7-12%: later waits for the B^T
 // fragments then also wait for those stores).
 //
-// Workgroups [0, plan.nfull) walk the whole chains bh = blockIdx.  Each of
-// the rest takes plan.seg_len chunks of one of the remaining chains (chains
-// nfull, nfull + 1, ...; plan.seg_per_chain segments each) and writes those
+// Workgroups [0, plan.nfull) walk one whole chain each (chains 0 .. nfull -
+// 1).  Each of the rest takes plan.seg_len chunks of one of the remaining
+// chains (chains nfull, nfull + 1, ...; plan.seg_per_chain segments each;
+// both ranges dealt out XCD by XCD, xcd_remap) and writes those
 // chunks' local states, exactly as chunk_state would (f32, or with the f16s
 // hand-over its f16 rows, SSD_STATE_F16S_LOCAL), for state_passing to
 // finish: with 1.25 chains per CU the whole chains take one workgroup slot
@@ -389,9 +390,15 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
   __builtin_assume(wave < kNW);
   const int g = lane >> 4, i = lane & 15;
   const bool local = (int)blockIdx.x >= plan.nfull;  // workgroup-uniform
-  int bh = blockIdx.x, c0 = 0, c1 = p.nchunks;     // chain b * nheads + h, chunks [c0, c1)
-  if (local) {
-    const int sg = (int)blockIdx.x - plan.nfull;
+  // Neighbouring chains (the heads of one batch row, which share B and its
+  // group's B^T fragments) go to one XCD's L2: workgroups are dealt to the
+  // XCDs in turn, so without the remap every fragment is fetched by all of
+  // them.  Whole chains and segments are remapped separately.
+  int bh = 0, c0 = 0, c1 = p.nchunks;  // chain b * nheads + h, chunks [c0, c1)
+  if (!local) {
+    bh = xcd_remap((int)blockIdx.x, plan.nfull);
+  } else {
+    const int sg = xcd_remap((int)blockIdx.x - plan.nfull, (int)gridDim.x - plan.nfull);
     bh = plan.nfull + sg / plan.seg_per_chain;
     c0 = (sg % plan.seg_per_chain) * plan.seg_len;
     c1 = min(c0 + plan.seg_len, p.nchunks);
