@@ -256,7 +256,14 @@ int ssd_chunk_scan(const ssd_dims* d, int dtype,
                    const void* prep, const ssd_epilogue* epilogue, void* stream);
 
 /* Whole SSD forward (K1, K0, K2, K3, K4 on one stream): the replacement for
- * SSDLayer._ssd_core (MR:123-162).  workspace must hold
+ * SSDLayer._ssd_core (MR:123-162).  Launches, all on `stream`: at chunk 256
+ * with 16-bit inputs K1 + K0 as one launch, then K2 + K3 as one state-chain
+ * launch (the chain's mixed plan adds K3 over the chains it leaves as
+ * segments) or K2 then K3 where the chains are too few, then K4: three or
+ * four.  At chunk 64 / 128 with f32 states, dstate 64 / 128 and chunk x
+ * dstate <= 8192: K1, the f32-state chain, K4.  With f32 states, dstate
+ * 16 / 32, chunk x dstate <= 2048 and at most 16 chunks: the whole forward in
+ * one launch.  Otherwise one launch per stage.  workspace must hold
  * ssd_workspace_bytes(d, state_dtype) bytes, 256-byte aligned (or that of
  * the chunk ssd_forward_chunk reports).  d->chunk is MR's block_len and only
  * has to divide L: for 16-bit inputs with f32 states (SSD_DTYPE_F32 or

@@ -26,9 +26,14 @@
 //     diagonal keeps the exact per-element form, masked before its exponent
 //     can overflow.
 //   * x^T operands come straight from row-major x in LDS through the
-//     transposing read ds_read_b64_tr_b16.  S_in (f32) is split once per item,
-//     in LDS, into a bf16 hi + lo pair that both go through the MFMA, so the
-//     state keeps ~16 significant bits.
+//     transposing read ds_read_b64_tr_b16.  S_in arrives, by default, as f16
+//     rows with a power-of-two scale per row (SSD_STATE_F16S, written so by
+//     state_passing or the state chain): one f16 MFMA per K step reads it as
+//     it lies, with C's rows held as f16 times their own power of two and
+//     both scales applied to the f32 result.  With state_format "split" it
+//     arrives as 16-bit (hi, lo) pairs of the input type (two MFMAs per K
+//     step, ~16 significant bits); plain f32 S_in is split so in LDS once per
+//     item.
 // Data movement.  The next item's x, S_in, Acs and dt are copied global ->
 // LDS by global_load_lds (no VGPRs held) into the second of two LDS buffers
 // while the current item computes; one wait + barrier per item publishes
@@ -38,8 +43,9 @@
 // uses a per-lane base computed once plus a compile-time offset.  y is stored
 // at the end of each item, 16 bytes per lane.
 //
-// Traffic per item: x 32 KB + S_in 32 KB (f32) + Acs 1 KB read, y 32 KB
-// written; B and C per group from L2.
+// Traffic per item: x 32 KB + S_in 16 KB (f16s; 32 KB as hi / lo pairs or
+// f32) + its row scales 256 B + Acs 1 KB read, y 32 KB written; B and C (or
+// chunk_prep's C.B^T fragments) per group from L2.
 //
 // Layer epilogue (EPI, with dt and chunk_prep's operands): y = (y + D[h] x)
 // * silu(z) (MR:116-118) before y's one rounding.  D x reads x from the
