@@ -225,23 +225,32 @@ def step_stats(fn, runs):
 
 
 def time_launches(fn, reps):
-    """Average device time (ms) of fn() over reps back-to-back launches.
+    """Average device time (ms) of fn() over reps back-to-back calls.
 
-    A short device-side sleep is queued first so the host can enqueue all
-    launches before the device reaches the start event: the events then bracket
-    device work only, not host launch latency.
+    A device-side sleep is queued first so the host can enqueue all calls
+    before the device reaches the start event: the events then bracket device
+    work only, not host launch latency.  The sleep is doubled and the calls
+    timed again while the host's enqueue outlasts it (fn may be several
+    Python-level launches).
     """
-    torch.cuda.synchronize()
     sleep = getattr(torch.cuda, "_sleep", None)
-    if sleep is not None:
-        sleep(20_000_000)
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for _ in range(reps):
-        fn()
-    end.record()
-    end.synchronize()
-    return start.elapsed_time(end) / reps
+    cycles = 20_000_000
+    while True:
+        torch.cuda.synchronize()
+        s0, start, end = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+        s0.record()
+        if sleep is not None:
+            sleep(cycles)
+        start.record()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            fn()
+        host_ms = (time.perf_counter() - t0) * 1e3
+        end.record()
+        end.synchronize()
+        if sleep is None or host_ms < 0.8 * s0.elapsed_time(start) or cycles >= 1_600_000_000:
+            return start.elapsed_time(end) / reps
+        cycles *= 2
 
 
 def cpu_baseline(cfg, budget_s=12.0, max_runs=30):
@@ -516,30 +525,34 @@ def main():
     model["ssd_small"] = dict(bytes=b_min, flops=f_min)
     kernels = {}
     pre_launches = 0
-    for name, fn in kfn.items():
-        fn()
-        ms = time_launches(fn, args.kernel_reps)
-        pre_launches += 1 + args.kernel_reps
+
+    def kernel_entry(name, ms):
         m = model[name]
         gbs = m["bytes"] / (ms * 1e-3) / 1e9
         tfs = m["flops"] / (ms * 1e-3) / 1e12
         t_hbm = m["bytes"] / (PEAK_HBM_GBS * 1e9)
         t_mfma = m["flops"] / (PEAK_TFLOPS[cfg.dtype] * 1e12)
-        kernels[name] = {
+        e = {
             "ms": round(ms, 5), "bytes": m["bytes"], "flops": m["flops"],
             "GB_s": round(gbs, 1), "TFLOP_s": round(tfs, 2),
             "hbm_frac": round(gbs / PEAK_HBM_GBS, 4), "mfma_frac": round(tfs / PEAK_TFLOPS[cfg.dtype], 4),
             "bound": "hbm" if t_hbm >= t_mfma else "mfma",
         }
         if "flops_cb_per_head" in m:
-            kernels[name]["flops_cb_per_head"] = m["flops_cb_per_head"]
-            kernels[name]["mfma_frac_cb_per_head"] = round(
-                m["flops_cb_per_head"] / (ms * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype], 4)
+            e["flops_cb_per_head"] = m["flops_cb_per_head"]
+            e["mfma_frac_cb_per_head"] = round(m["flops_cb_per_head"] / (ms * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype], 4)
         executed = profiled_mfma(cfg, name)
         if executed is not None:
             # the flops the MFMA instructions of one launch perform (rocprofv3
             # SQ_INSTS_MFMA), over this run's time
-            kernels[name]["mfma_executed_frac"] = round(executed / (ms * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype], 4)
+            e["mfma_executed_frac"] = round(executed / (ms * 1e-3) / 1e12 / PEAK_TFLOPS[cfg.dtype], 4)
+        return e
+
+    # each kernel alone, back to back on its own inputs
+    for name, fn in kfn.items():
+        fn()
+        kernels[name] = kernel_entry(name, time_launches(fn, args.kernel_reps))
+        pre_launches += 1 + args.kernel_reps
     # the dominant kernel among those the forward runs: K2 + K3 as it runs them
     # (chunk_state_passing), K4, K1 and K0 -- not the standalone chunk_state
     # and state_passing rows, which stand in for it only as a breakdown
