@@ -354,6 +354,27 @@ def test_small_state_forward(dtype, Q, N, nc, h, g, opts):
     assert_close(final, fs, tol)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("Q,N", [(64, 16), (64, 32), (128, 16)])
+def test_small_state_forward_one_workgroup_per_chain(dtype, Q, N):
+    """The one-launch forward with at least twice as many (b, h) chains as
+    CUs (32 x 16 = 512 on 256 CUs): one workgroup per chain instead of two
+    halves of P.  Against the fp64 sequential scan, with dt and an initial
+    state."""
+    say("small-state fwd, whole chains", dtype, Q, N)
+    b, h, g, nc = 32, 16, 4, 3
+    cfg, inp = small_case(dtype, Q, N, b=b, nc=nc, h=h, g=g, init=True)
+    dt = torch.rand(b, nc * Q, h, generator=torch.Generator().manual_seed(7)) + 0.5
+    d = to_dev(inp)
+    Y, final = S.ssd_forward(d["X"], d["A"], d["B"], d["C"], Q, dt=dt.to(DEV), initial_states=d["init"],
+                             return_final_states=True)
+    torch.cuda.synchronize()
+    Ys, fs = O.ssd_sequential(inp["X"], inp["A"], inp["B"], inp["C"], dt=dt, initial_states=inp["init"])
+    tol = tolerance(dtype)
+    assert_close(Y, Ys, tol)
+    assert_close(final, fs, tol)
+
+
 def test_forward_bf16_states():
     say("fwd bf16 states")
     cfg, inp = small_case(torch.bfloat16, 256, 128, b=2, nc=4, h=4, g=1, init=True)

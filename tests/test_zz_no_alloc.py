@@ -2,8 +2,9 @@
 is a device array the library keeps per device) against ssd_forward with a
 caller-allocated workspace: the same kernels, so the same bits.  Two calls in
 a row, the second smaller; a call whose workspace exceeds the array (run in
-batch slices); an f32 call on the generic kernels; and a shape whose single
-batch element does not fit, rejected on the host before any launch.
+batch slices); an f32 call on the generic kernels; the one-launch forward
+for small states; and a shape whose single batch element does not fit,
+rejected on the host before any launch.
 
 A batch slice has fewer (batch, head) chains than the whole call, and at
 chunk 256 the chain count picks how K2 + K3 run: one state-chain launch with
@@ -98,6 +99,16 @@ def test_noalloc_f32_generic_kernels():
     cfg = CONFIGS["C5"].scaled(batch=4)
     print("CASE noalloc f32", cfg, flush=True)
     Y0, f0, Y1, f1 = run_both(cfg, 3, use_dt=True)
+    assert torch.equal(Y1, Y0) and torch.equal(f1, f0)
+
+
+def test_noalloc_one_launch_small_states():
+    """C1 (d_state 16, two chunks per chain): the whole forward is one
+    launch that uses no workspace; the no-alloc entry point runs the same."""
+    cfg = CONFIGS["C1"]
+    print("CASE noalloc one launch", cfg, flush=True)
+    assert S.workspace_bytes(cfg.batch, cfg.seqlen, cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, cfg.chunk) == 256
+    Y0, f0, Y1, f1 = run_both(cfg, 4, use_dt=True)
     assert torch.equal(Y1, Y0) and torch.equal(f1, f0)
 
 
