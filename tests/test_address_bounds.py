@@ -256,16 +256,19 @@ def test_chunk_state_q256_and_chain_addresses(name):
         "if (wave < kQ / 64) dma4_at(dchain + (l0 + 64 * wave + lane) * p.sdl, dr_lds + (uint32_t)((bs * kQ + 64 * wave) * 4));",
         "((((int64_t)b * p.nchunks + c) * p.ngroups + grp) * NTILE + nt) * (kKS * 64) + lane;",
         "const frag8<T>* bnext = btf_of(has_next ? c + 1 : c);",
-        "*reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;",
+        "const int row = 16 * (pt0 + 2 * u + (odd ? 1 : 0)) + i;",
+        "*reinterpret_cast<u32x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * (g & ~1)) =",
         "sp.sscale[(((int64_t)b * p.nchunks + c) * p.nheads + h) * kP + row] = __builtin_ldexpf(1.f, e);",
+        "const int row = row0 + 16 * (g & 1);",
+        "store_f16l<N>(reinterpret_cast<float*>(sg), 16 * (pt0 + 2 * k) + i, nt, g, st_prev[2 * k], st_prev[2 * k + 1]);",
+        "for (int u = 0; u < PTW / 2; ++u) store_f16l<N>(sg, 16 * (pt0 + 2 * u) + i, nt, g, st[2 * u], st[2 * u + 1]);",
         "bh = xcd_remap((int)blockIdx.x, plan.nfull);",
         "const int sg = xcd_remap((int)blockIdx.x - plan.nfull, (int)gridDim.x - plan.nfull);",
         "bh = plan.nfull + sg / plan.seg_per_chain;",
         "c0 = (sg % plan.seg_per_chain) * plan.seg_len;",
         "c1 = min(c0 + plan.seg_len, p.nchunks);",
         "if (c0 >= c1) return;  // the whole workgroup, before any barrier",
-        "*reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;",
-        "if (g == 0) item[f16l_scale_slot<N>(row, nt)] = __builtin_ldexpf(1.f, e);")
+        "if (g == 0) item[f16l_scale_slot<N>(row0 + 16 * s, nt)] = __builtin_ldexpf(1.f, e);")
     wave, lane = lanes()
     g, i = lane >> 4, lane & 15
     nt, pt0 = wave % NT, (wave // NT) * PTW
@@ -275,6 +278,26 @@ def test_chunk_state_q256_and_chain_addresses(name):
     inside("state columns", 16 * nt + 4 * g + 3, 0, N)
     inside("f16s: f16 columns in the row's first half", 16 * nt + 4 * g + 3, 0, N)
     inside("f16s scales rows", 16 * (pt0 + q) + i, 0, P)
+    # 16-byte stores of a tile pair (2u, 2u + 1): row of tile 2u + (g & 1),
+    # columns 16 nt + 4 (g & ~1) .. + 7, 16-byte aligned in the row's f16 half
+    u = np.arange(PTW // 2)[:, None, None]
+    prow = 16 * (pt0 + 2 * u + (g & 1)) + i
+    pcol = 16 * nt + 4 * (g & ~1)
+    inside("pair store rows", prow, 0, P)
+    inside("pair store columns (f16)", pcol + 7, 0, N)
+    assert ((pcol * 2) % 16 == 0).all()
+    # every (row, column) of the item written exactly once by the 8 waves' pair stores
+    seen = np.zeros((P, N), np.int64)
+    for wv in range(8):
+        ntw, pt0w = wv % NT, (wv // NT) * PTW
+        for uu in range(PTW // 2):
+            for ln in range(64):
+                gg, ii = ln >> 4, ln & 15
+                r = 16 * (pt0w + 2 * uu + (gg & 1)) + ii
+                c0 = 16 * ntw + 4 * (gg & ~1)
+                seen[r, c0:c0 + 8] += 1
+    if NT == 8:  # the f16s chain store needs one n tile per wave (d_state 128)
+        assert (seen == 1).all()
     # K2's f16 local states: f16 columns in the row's first half, the tile
     # scales packed into the second halves of the item's first rows (every
     # (row, tile)'s slot distinct, none in an f16 half)

@@ -34,6 +34,9 @@
 // (MR:148-149 itself forms the states in the inputs' 16-bit type and MR:155
 // stores them in float16).  A tile row lies in one wave (lanes i, i + 16,
 // i + 32, i + 48 hold its 16 states), so its maximum takes two lane swaps.
+// Two p tiles are stored together: lane groups g, g + 1 swap halves of their
+// values, so that each lane writes 8 consecutive f16 (one 16-byte store per
+// lane and tile pair instead of two 8-byte ones).
 #include <climits>
 #include <type_traits>
 
@@ -88,24 +91,40 @@ __device__ __forceinline__ Item next_item(const ChunkStateArgs& p, Item r, int h
   return r;
 }
 
-// SSD_STATE_F16S_LOCAL store of one lane's 4 local states: row `row`,
-// columns 16 nt + 4 g .. + 3 of the [P][N] item at `item` (f32 layout).  The
-// 16 states of the row in n tile nt are in lanes i, i + 16, i + 32, i + 48
-// (i = row % 16) of the wave: their largest magnitude takes two lane swaps,
-// and sets the tile row's power-of-two scale (largest |v| in [2^14, 2^15]).
+// SSD_STATE_F16S_LOCAL store of one lane's local states of two p tiles: rows
+// row0 (tile 2u) and row0 + 16 (tile 2u + 1), columns 16 nt + 4 g .. + 3 of
+// the [P][N] item at `item` (f32 layout), 4 values each.  The 16 states of a
+// row in n tile nt are in lanes i, i + 16, i + 32, i + 48 (i = row % 16) of
+// the wave: their largest magnitude takes two lane swaps, and sets the tile
+// row's power-of-two scale (largest |v| in [2^14, 2^15]).  Lane groups g,
+// g + 1 (g even) then swap halves so that each lane writes 8 consecutive f16
+// (one 16-byte store): the even group tile 2u's row, the odd one tile
+// 2u + 1's.
 template <int N>
-__device__ __forceinline__ void store_f16l(float* item, int row, int nt, int g, f32x4 v) {
-  float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
-  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-  m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-  m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-  const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
-  f16x4 hv;
+__device__ __forceinline__ void store_f16l(float* item, int row0, int nt, int g, f32x4 v0, f32x4 v1) {
+  typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+  typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+  u32x2 hw[2];
 #pragma unroll
-  for (int k = 0; k < 4; ++k) hv[k] = (f16)__builtin_ldexpf(v[k], -e);
-  *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;
-  if (g == 0) item[f16l_scale_slot<N>(row, nt)] = __builtin_ldexpf(1.f, e);
+  for (int s = 0; s < 2; ++s) {
+    const f32x4 v = s ? v1 : v0;
+    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
+    m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+    const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
+    f16x4 hv;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) hv[k] = (f16)__builtin_ldexpf(v[k], -e);
+    hw[s] = __builtin_bit_cast(u32x2, hv);
+    if (g == 0) item[f16l_scale_slot<N>(row0 + 16 * s, nt)] = __builtin_ldexpf(1.f, e);
+  }
+  const auto w0 = __builtin_amdgcn_permlane16_swap(hw[0][0], hw[1][0], false, false);
+  const auto w1 = __builtin_amdgcn_permlane16_swap(hw[0][1], hw[1][1], false, false);
+  const int row = row0 + 16 * (g & 1);
+  *reinterpret_cast<u32x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * (g & ~1)) =
+      u32x4{w0[0], w1[0], w0[1], w1[1]};
 }
 
 template <typename S> struct StateStore;
@@ -249,12 +268,15 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
   };
 
   f32x4 st_prev[PTW];
-  auto store_state = [&](const Item& r, int q) __attribute__((always_inline)) {
+  // store k of the previous item's states: tile q = k, or with F16L the tile
+  // pair (2k, 2k + 1)
+  constexpr int NSTORE = F16L ? PTW / 2 : PTW;
+  auto store_state = [&](const Item& r, int k) __attribute__((always_inline)) {
     S* sg = reinterpret_cast<S*>(p.states) + (((int64_t)r.b * p.nchunks + r.c) * p.nheads + r.h) * (int64_t)(kP * N);
     if constexpr (F16L) {
-      store_f16l<N>(reinterpret_cast<float*>(sg), 16 * (pt0 + q) + i, nt, g, st_prev[q]);
+      store_f16l<N>(reinterpret_cast<float*>(sg), 16 * (pt0 + 2 * k) + i, nt, g, st_prev[2 * k], st_prev[2 * k + 1]);
     } else {
-      StateStore<S>::store(sg + srow + 16 * N * q, st_prev[q]);
+      StateStore<S>::store(sg + srow + 16 * N * k, st_prev[k]);
     }
   };
 
@@ -288,7 +310,7 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
       compute(bc, [&](int ks) __attribute__((always_inline)) {
         if (ks < kXBlocks / kNW) {
           if (has_next) issue_copy_part(nxt, bn, ks);
-        } else if (ks - kXBlocks / kNW < PTW) {
+        } else if (ks - kXBlocks / kNW < NSTORE) {
           if (has_prev) store_state(prev, ks - kXBlocks / kNW);
         }
       });
@@ -316,7 +338,7 @@ void chunk_state_q256_kernel(ChunkStateArgs p) {
   }
   if (any) {
 #pragma unroll
-    for (int q = 0; q < PTW; ++q) store_state(prev, q);
+    for (int k = 0; k < NSTORE; ++k) store_state(prev, k);
   }
 }
 
@@ -505,32 +527,49 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
   };
   auto store_sin_f16s = [&](int c, int par) __attribute__((always_inline)) {
     float* item = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (int64_t)(kP * N);
+    // one p-tile pair (2u, 2u + 1) at a time: lane groups g, g + 1 (g even)
+    // swap halves, so the even group holds columns 16 nt + 4 g .. + 7 of tile
+    // 2u's row and the odd one those of tile 2u + 1's row (one 16-byte store each)
 #pragma unroll
-    for (int q = 0; q < PTW; ++q) {
-      const int row = 16 * (pt0 + q) + i;
-      const f32x4 m0 = *reinterpret_cast<const f32x4*>(&rmx[par][row][0]);
-      const f32x4 m1 = *reinterpret_cast<const f32x4*>(&rmx[par][row][4]);
-      const float m = fmaxf(fmaxf(fmaxf(m0[0], m0[1]), fmaxf(m0[2], m0[3])),
-                            fmaxf(fmaxf(m1[0], m1[1]), fmaxf(m1[2], m1[3])));
-      const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
-      f32x4 v = st[q];
-      asm volatile("" : "+v"(v));  // from the f32 state (no fusing of the recurrence into the rounding)
-      f16x4 hv;
+    for (int u = 0; u < PTW / 2; ++u) {
+      u32x2 hw[2];
 #pragma unroll
-      for (int k = 0; k < 4; ++k) hv[k] = (f16)__builtin_ldexpf(v[k], -e);
-      *reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * g) = hv;
-      if (wave == 0 && g == 0)
-        sp.sscale[(((int64_t)b * p.nchunks + c) * p.nheads + h) * kP + row] = __builtin_ldexpf(1.f, e);
+      for (int s = 0; s < 2; ++s) {
+        const int q = 2 * u + s, row = 16 * (pt0 + q) + i;
+        const f32x4 m0 = *reinterpret_cast<const f32x4*>(&rmx[par][row][0]);
+        const f32x4 m1 = *reinterpret_cast<const f32x4*>(&rmx[par][row][4]);
+        const float m = fmaxf(fmaxf(fmaxf(m0[0], m0[1]), fmaxf(m0[2], m0[3])),
+                              fmaxf(fmaxf(m1[0], m1[1]), fmaxf(m1[2], m1[3])));
+        const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
+        f32x4 v = st[q];
+        asm volatile("" : "+v"(v));  // from the f32 state (no fusing of the recurrence into the rounding)
+        f16x4 hv;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) hv[k] = (f16)__builtin_ldexpf(v[k], -e);
+        hw[s] = __builtin_bit_cast(u32x2, hv);
+        if (wave == 0 && g == 0)
+          sp.sscale[(((int64_t)b * p.nchunks + c) * p.nheads + h) * kP + row] = __builtin_ldexpf(1.f, e);
+      }
+      const auto w0 = __builtin_amdgcn_permlane16_swap(hw[0][0], hw[1][0], false, false);
+      const auto w1 = __builtin_amdgcn_permlane16_swap(hw[0][1], hw[1][1], false, false);
+      const int row = 16 * (pt0 + 2 * u + (odd ? 1 : 0)) + i;
+      *reinterpret_cast<u32x4*>(reinterpret_cast<f16*>(item + (int64_t)row * N) + 16 * nt + 4 * (g & ~1)) =
+          u32x4{w0[0], w1[0], w0[1], w1[1]};
     }
   };
 
   // a segment's local state of chunk c in chunk_state's layout: f32, or with
   // the f16s hand-over as chunk_state's f16 rows (SSD_STATE_F16S_LOCAL) for
   // state_passing to finish
-  auto store_local = [&](int c, int q) __attribute__((always_inline)) {
+  auto store_local = [&](int c) __attribute__((always_inline)) {
     float* sg = reinterpret_cast<float*>(sp.states) + (((int64_t)b * p.nchunks + c) * p.nheads + h) * (int64_t)(kP * N);
-    if constexpr (F16S) store_f16l<N>(sg, 16 * (pt0 + q) + i, nt, g, st[q]);
-    else *reinterpret_cast<f32x4*>(sg + srow + 16 * N * q) = st[q];
+    if constexpr (F16S) {
+#pragma unroll
+      for (int u = 0; u < PTW / 2; ++u) store_f16l<N>(sg, 16 * (pt0 + 2 * u) + i, nt, g, st[2 * u], st[2 * u + 1]);
+    } else {
+#pragma unroll
+      for (int q = 0; q < PTW; ++q) *reinterpret_cast<f32x4*>(sg + srow + 16 * N * q) = st[q];
+    }
   };
 
   frag8<T> bt[kKS];
@@ -582,8 +621,7 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
     if (local) {
 #pragma unroll
       for (int q = 0; q < PTW; ++q) st[q] = acc[q];
-#pragma unroll
-      for (int q = 0; q < PTW; ++q) store_local(c, q);
+      store_local(c);
     } else if constexpr (F16S) {
       store_sin_f16s(c, c & 1);
 #pragma unroll
