@@ -6,7 +6,7 @@
 // compute it (workloads/mamba/model_ref.py:135-162):
 //   Acs[l]   = sum_{k<=l} A[k]                    (MR:135-136; K1's scan order)
 //   W[l][s]  = exp(Acs[l] - Acs[s]) dt[s] (C_l . B_s) for s <= l, else 0
-//                                                 (MR:139-144; masked before the exp)
+//                                                 (MR:139-144; 0 by selection above the diagonal)
 //   y[l][p]  = sum_{s<=l} W[l][s] x[s][p] + exp(Acs[l]) sum_n C[l][n] S[p][n]
 //                                                 (MR:145, 160-162)
 //   S[p][n] <- exp(Acs[Q-1]) S[p][n] + sum_l x[l][p] dt[l] exp(Acs[Q-1] - Acs[l]) B[l][n]
@@ -193,9 +193,9 @@ __global__ __launch_bounds__(kT) void ssd_small_kernel(SmallArgs p) {
     if (c + 1 < p.nchunks) fetch(c + 1);  // lands while this chunk computes
 
     // W on the causal 16 x 16 tiles (row tile r, column tile cc <= r): C.B^T
-    // over n, then exp(Acs[l] - Acs[s]) dt[s]; the exp is never evaluated
-    // above the diagonal (positive log-decays cannot overflow there), where
-    // the entries are 0
+    // over n, then exp(Acs[l] - Acs[s]) dt[s]; above the diagonal the entries
+    // are 0 by selection, so an exponent that overflows there (positive
+    // log-decays) is discarded, never multiplied into W
     for (int tau = wave; tau < R * (R + 1) / 2; tau += 4) {
       int r = 0;
       while ((r + 1) * (r + 2) / 2 <= tau) ++r;
