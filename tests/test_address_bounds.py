@@ -723,7 +723,7 @@ def test_state_passing_addresses(name):
         "if (v >= vec_per_bh) return;",
         "const int row = v / TPR, col = SPT * (v % TPR);",
         "float* elem = base + SPT * (int64_t)v;",
-        "*reinterpret_cast<H*>(hrow + c * 2 * cstride) = hv;",
+        "__builtin_nontemporal_store(hv, reinterpret_cast<H*>(hrow + c * 2 * cstride));",
         "constexpr int spt = 8, unroll = 2;",
         "const int c = min(c0 + u, nchunks - 1);",
         "const float* rscale = base + f16l_scale_slot<N>(row, col / 16);",

@@ -282,7 +282,10 @@ __global__ __launch_bounds__(256) void state_passing_f16s_kernel(StatePassingArg
     H hv;
 #pragma unroll
     for (int k = 0; k < SPT; ++k) hv[k] = (f16)__builtin_ldexpf(val[k], -e);
-    *reinterpret_cast<H*>(hrow + c * 2 * cstride) = hv;
+    // non-temporal: S_in is read once, by chunk_scan after this launch (C4's
+    // forward 884 -> 875 us; C3's, whose K3 covers only the mixed plan's
+    // segment chains, unchanged)
+    __builtin_nontemporal_store(hv, reinterpret_cast<H*>(hrow + c * 2 * cstride));
     if (col == 0) srow[c * sstride] = __builtin_ldexpf(1.f, e);
   };
   // F16L: this thread's SPT f16 local values of chunk c times the row's scale
