@@ -4,6 +4,7 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3]
                     [--state-dtype f32|bf16] [--no-cpu-baseline]
     python bench.py --layer [--steps K] [--warmup W]
+    python bench.py --decode [--decode-batches 4,64,256]
 
 A step is one SSD forward (K1 cumsum and K0 chunk_prep in one launch -> K2
 chunk_state and K3 state_passing, one launch per (b, h) chain where that is
@@ -32,6 +33,10 @@ weights): the whole ``SSDLayer.forward``, and separately the span between
 its two projections, once as libssd's single ``ssd_layer`` call and once as
 PyTorch glue (conv1d, SiLU, softplus, skip, gate) around ``ssd_forward``.
 It prints one JSON line of its own; the headline line above is unaffected.
+
+``--decode`` times one decode step (``ssd_decode_step``, one token of the
+recurrence in place on the f32 state) at C3's head shape for a few batch
+sizes, with the state's HBM bytes per step over the step's device time.
 """
 
 from __future__ import annotations
@@ -407,6 +412,54 @@ def layer_bench(args):
     print(json.dumps(out), flush=True)
 
 
+def decode_bench(args):
+    """One decode step (ssd_decode_step: one token of the recurrence, in place
+    on the [b, h, P, N] f32 state) at C3's head shape for each batch size in
+    args.decode_batches.  Algorithmic bytes per step: the state read and
+    written once (8 bytes per element), x and y (P values per head), B and C
+    (N per group), a and dt (f32 per head).  Two states are used in turn, so
+    that from 64 batch rows on (2 x 168 MB) the state does not stay in the
+    256 MB Infinity Cache between steps."""
+    cfg = CONFIGS[HEADLINE]
+    h, P, N, g, dt_ = cfg.nheads, cfg.headdim, cfg.dstate, cfg.ngroups, cfg.dtype
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    es = esize(dt_)
+    rows = []
+    for b in args.decode_batches:
+        states = [torch.randn(b, h, P, N, device=dev, generator=gen) for _ in range(2)]
+        x = torch.randn(b, h, P, device=dev, generator=gen).to(dt_)
+        Bm = torch.randn(b, g, N, device=dev, generator=gen).to(dt_)
+        Cm = torch.randn(b, g, N, device=dev, generator=gen).to(dt_)
+        a = -torch.rand(b, h, device=dev, generator=gen) * 0.1
+        dt = torch.rand(b, h, device=dev, generator=gen) * 0.1
+        k = [0]
+
+        def step():
+            i = k[0] % 2
+            k[0] += 1
+            return S.decode_step(states[i], x, Bm, Cm, a, dt)
+
+        step()
+        ms = time_launches(step, args.kernel_reps)
+        nbytes = b * h * P * N * 8 + 2 * b * h * P * es + 2 * b * g * N * es + 2 * b * h * 4
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        rows.append({"batch": b, "us_per_step": round(ms * 1e3, 2), "tokens_per_s": round(b / (ms * 1e-3), 1),
+                     "algorithmic_bytes": nbytes, "GB_s": round(gbs, 1), "hbm_frac": round(gbs / PEAK_HBM_GBS, 4)})
+        del states
+    out = {
+        "metric": "SSD decode step (one token, in place on the f32 state), 1 MI355X",
+        "dtype": DTYPE_NAMES[dt_] + " inputs, f32 state",
+        "data": "synthetic",
+        "config": {"workload": "decode at C3's head shape", "nheads": h, "headdim": P, "dstate": N, "ngroups": g},
+        "reps": args.kernel_reps,
+        "roofline_peak_GB_s": PEAK_HBM_GBS,
+        "steps": rows,
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -420,6 +473,10 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=30)
     ap.add_argument("--layer", action="store_true",
                     help="time one full layer at the reference module's production shape instead")
+    ap.add_argument("--decode", action="store_true",
+                    help="time one decode step (ssd_decode_step) at C3's head shape instead, per batch size")
+    ap.add_argument("--decode-batches", type=lambda v: [int(t) for t in v.split(",")], default=[4, 64, 256],
+                    metavar="B1,B2,..", help="batch sizes for --decode (default 4,64,256)")
     ap.add_argument("--copy-probe", type=int, default=0, metavar="MB",
                     help="only run a plain device-to-device copy of MB MiB (5 times) and exit: the "
                          "reference point that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings to bytes")
@@ -441,6 +498,10 @@ def main():
 
     if args.hbm_probe:
         hbm_probe(args)
+        return
+
+    if args.decode:
+        decode_bench(args)
         return
 
     if args.copy_probe:

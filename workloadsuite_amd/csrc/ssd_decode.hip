@@ -48,30 +48,35 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs p) {
   float* sg = p.state + ((int64_t)b * p.nheads + h) * (int64_t)(kP * N);
   const float dsk = p.dskip ? p.dskip[h] : 0.f;
   const T* zg = p.z ? static_cast<const T*>(p.z) + (int64_t)b * p.szb + (int64_t)h * p.szh : nullptr;
+  f32x4 st[ITERS];
+  float xv[ITERS], zr[ITERS];
 
+  // every load of the wave's rows first (ITERS 16-byte state loads in flight
+  // per lane instead of one round trip per row), then the updates and stores
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     const int row = 16 * wave + RPI * it + rsub;
-    float* sp = sg + row * N + n4;
-    const f32x4 s = *reinterpret_cast<const f32x4*>(sp);
-    const float xv = to_f32<T>(xg[row]);
-    const float u = dt * xv;
+    st[it] = *reinterpret_cast<const f32x4*>(sg + row * N + n4);
+    xv[it] = to_f32<T>(xg[row]);
+    if (zg) zr[it] = to_f32<T>(zg[row]);
+  }
+#pragma unroll
+  for (int it = 0; it < ITERS; ++it) {
+    const int row = 16 * wave + RPI * it + rsub;
+    const float u = dt * xv[it];
     f32x4 ns;
     float part = 0.f;
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      ns[k] = da * s[k] + u * bv[k];
+      ns[k] = da * st[it][k] + u * bv[k];
       part += cv[k] * ns[k];
     }
-    *reinterpret_cast<f32x4*>(sp) = ns;
+    *reinterpret_cast<f32x4*>(sg + row * N + n4) = ns;
 #pragma unroll
     for (int off = LPR / 2; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
     if (lane % LPR == 0) {
-      float v = part + dsk * xv;
-      if (zg) {
-        const float zv = to_f32<T>(zg[row]);
-        v *= zv / (1.f + expf(-zv));
-      }
+      float v = part + dsk * xv[it];
+      if (zg) v *= zr[it] / (1.f + expf(-zr[it]));
       yg[row] = from_f32<T>(v);
     }
   }
