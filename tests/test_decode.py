@@ -144,3 +144,48 @@ def test_decode_several_steps_after_forward(k, dtype, Q, N, g, h, b):
     scale = float(np.abs(fs).max())
     f16l = dtype != torch.float32 and Q == 256 and N in (64, 128) and f16_local(b * h, N)
     close(state / scale, fs / scale, 2e-3 if f16l else 1e-4)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_decode_full_size_sampled(dtype):
+    """One decode step at C3's head shape with 256 batch rows (the largest
+    shape bench.py --decode times: 20480 workgroups, a 671 MB state), with the
+    skip and gate: sampled (batch, head) pairs against the float64 per-token
+    update state' = exp(a) state + dt x B^T, y = (C . state' + D x) silu(z)
+    (MR:152-161's per-token form, MR:116-118's epilogue), and every other
+    state row unchanged in its update rule (checked through the state's
+    checksum over all rows: sum state' = exp(a) sum state + dt (sum x)(sum B))."""
+    say("decode full size", dtype)
+    b, h, P, N, g = 256, 80, 64, 128, 1
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    state = torch.randn(b, h, P, N, device=DEV, generator=gen)
+    x = torch.randn(b, h, P, device=DEV, generator=gen).to(dtype)
+    z = torch.randn(b, h, P, device=DEV, generator=gen).to(dtype)
+    Bm = (torch.randn(b, g, N, device=DEV, generator=gen) * N ** -0.5).to(dtype)
+    Cm = (torch.randn(b, g, N, device=DEV, generator=gen) * N ** -0.5).to(dtype)
+    a = -torch.rand(b, h, device=DEV, generator=gen) * 0.2
+    dt = torch.rand(b, h, device=DEV, generator=gen) * 0.5 + 0.05
+    D = torch.randn(h, device=DEV, generator=gen)
+    s0 = state.double()
+    # per-(b, h) checksums of the state before the step, for the size-independent check
+    sum0 = s0.sum(dim=(2, 3))
+    y = S.decode_step(state, x, Bm, Cm, a, dt=dt, D=D, z=z)
+    torch.cuda.synchronize()
+    ea = torch.exp(a.double())
+    xs, Bs = x.double(), Bm.double()
+    # every row: sum_p,n state' = exp(a) sum state + dt (sum_p x)(sum_n B)
+    want = ea * sum0 + dt.double() * xs.sum(-1) * Bs[:, 0].sum(-1)[:, None]
+    got = state.double().sum(dim=(2, 3))
+    scale = float(s0.abs().sum(dim=(2, 3)).max())
+    assert float((got - want).abs().max()) <= 1e-5 * scale
+    # sampled pairs in full, in float64
+    pick = torch.Generator().manual_seed(11)
+    bs = torch.randint(b, (12,), generator=pick).tolist()
+    hs = torch.randint(h, (12,), generator=pick).tolist()
+    for bi, hi in zip(bs, hs):
+        sn = ea[bi, hi] * s0[bi, hi] + dt[bi, hi].double() * xs[bi, hi][:, None] * Bs[bi, 0][None, :]
+        close(state[bi, hi], sn, 1e-5)
+        zz = z[bi, hi].double()
+        yr = (sn @ Cm[bi, 0].double() + D[hi].double() * xs[bi, hi]) * zz * torch.sigmoid(zz)
+        close(y[bi, hi], yr, tolerance(dtype))
