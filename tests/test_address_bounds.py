@@ -462,7 +462,7 @@ def test_f32_kernel_addresses(name):
         "if (g == 0) rmax[buf][(wave >> 1) * kP + 16 * (2 * pp + a) + i] = m;",
         "const float* rm = rmax[c & 1];",
         "const int pr = 16 * (2 * pp + a) + i;",
-        "const float m = fmaxf(fmaxf(rm[pr], rm[kP + pr]), fmaxf(rm[2 * kP + pr], rm[3 * kP + pr]));",
+        "const float m = nn_max(nn_max(rm[pr], rm[kP + pr]), nn_max(rm[2 * kP + pr], rm[3 * kP + pr]));",
         "*reinterpret_cast<f16x4*>(reinterpret_cast<f16*>(sg + pr * N) + 16 * (nt0 + n) + 4 * g) = hv;",
         "sp.sscale[(((int64_t)b * p.nchunks + c) * p.nheads + h) * kP + pr] = __builtin_ldexpf(1.f, e);")
     wave, lane = lanes()

@@ -224,8 +224,8 @@ __global__ __launch_bounds__(kThreads) void chunk_scan_b16_kernel(ChunkScanArgs 
       }
       float m = __uint_as_float(min(mb, 0x7f80u) << 16);  // a NaN counts as inf, as in every lane
       // the row's 4 lane groups (lanes i, i + 16, i + 32, i + 48)
-      m = fmaxf(m, __shfl_xor(m, 16));
-      m = fmaxf(m, __shfl_xor(m, 32));
+      m = nn_max(m, __shfl_xor(m, 16));
+      m = nn_max(m, __shfl_xor(m, 32));
       const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
       cs[r] = __builtin_ldexpf(1.f, e);
 #pragma unroll

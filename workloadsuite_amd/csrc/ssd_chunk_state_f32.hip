@@ -338,9 +338,9 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
 #pragma unroll
         for (int k = 0; k < 4; ++k) m = fmaxf(m, fabsf(st[a][n][k]));
       const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-      m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+      m = nn_max(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
       const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-      m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+      m = nn_max(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
       if (g == 0) rmax[buf][(wave >> 1) * kP + 16 * (2 * pp + a) + i] = m;
     }
   };
@@ -378,7 +378,7 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
 #pragma unroll
       for (int a = 0; a < 2; ++a) {
         const int pr = 16 * (2 * pp + a) + i;
-        const float m = fmaxf(fmaxf(rm[pr], rm[kP + pr]), fmaxf(rm[2 * kP + pr], rm[3 * kP + pr]));
+        const float m = nn_max(nn_max(rm[pr], rm[kP + pr]), nn_max(rm[2 * kP + pr], rm[3 * kP + pr]));
         const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
 #pragma unroll
         for (int n = 0; n < NTW; ++n) {

@@ -110,9 +110,9 @@ __device__ __forceinline__ void store_f16l(float* item, int row0, int nt, int g,
     const f32x4 v = s ? v1 : v0;
     float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
     const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-    m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    m = nn_max(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
     const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-    m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+    m = nn_max(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
     const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
     f16x4 hv;
 #pragma unroll
@@ -518,9 +518,9 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
       // the neighbouring 16-lane row, then with the other 32-lane half
       {
         const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-        m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+        m = nn_max(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
         const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-        m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+        m = nn_max(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
       }
       if (g == 0) rmx[par][16 * (pt0 + q) + i][wave] = m;
     }
@@ -538,8 +538,8 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
         const int q = 2 * u + s, row = 16 * (pt0 + q) + i;
         const f32x4 m0 = *reinterpret_cast<const f32x4*>(&rmx[par][row][0]);
         const f32x4 m1 = *reinterpret_cast<const f32x4*>(&rmx[par][row][4]);
-        const float m = fmaxf(fmaxf(fmaxf(m0[0], m0[1]), fmaxf(m0[2], m0[3])),
-                              fmaxf(fmaxf(m1[0], m1[1]), fmaxf(m1[2], m1[3])));
+        const float m = nn_max(nn_max(nn_max(m0[0], m0[1]), nn_max(m0[2], m0[3])),
+                               nn_max(nn_max(m1[0], m1[1]), nn_max(m1[2], m1[3])));
         const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
         f32x4 v = st[q];
         asm volatile("" : "+v"(v));  // from the f32 state (no fusing of the recurrence into the rounding)

@@ -103,6 +103,16 @@ __device__ __forceinline__ void split_weighted(const frag8<T>& b, f32x4 w0, f32x
   }
 }
 
+// Larger of two non-negative floats (magnitudes, or maxima of magnitudes)
+// as an unsigned integer max of their bits: for non-negative IEEE values the
+// order of the bit patterns is the numeric order, so a finite result is
+// fmaxf's, without the quieting max(x, x) the compiler puts in front of
+// fmaxf for a value read from memory or moved across lanes (a NaN, whose bits
+// lie above infinity's, wins where fmaxf would drop it).
+__device__ __forceinline__ float nn_max(float a, float b) {
+  return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
+}
+
 // SSD_STATE_F16S_LOCAL: the f32 slot, within a [P][N] item, that holds the
 // scale of row p's n tile t (columns 16 t .. 16 t + 15) -- the item's
 // P x N/16 scales, in (p, t) order, packed into the second halves (unused by

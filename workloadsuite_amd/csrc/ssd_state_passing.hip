@@ -202,14 +202,14 @@ __device__ __forceinline__ float row_max(float m) {
       default: return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x140, 0xF, 0xF, false)); // row_mirror
     }
   };
-  m = fmaxf(m, dpp(m, 0));
-  m = fmaxf(m, dpp(m, 1));
-  m = fmaxf(m, dpp(m, 2));
-  if constexpr (G >= 16) m = fmaxf(m, dpp(m, 3));
+  m = nn_max(m, dpp(m, 0));
+  m = nn_max(m, dpp(m, 1));
+  m = nn_max(m, dpp(m, 2));
+  if constexpr (G >= 16) m = nn_max(m, dpp(m, 3));
   if constexpr (G == 32) {
     // with the neighbouring 16-lane row
     const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
-    m = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+    m = nn_max(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
   }
   return m;
 }
