@@ -336,7 +336,7 @@ __global__ __launch_bounds__(kThreads) void chunk_state_chain_f32_kernel(ChunkSt
 #pragma unroll
       for (int n = 0; n < NTW; ++n)
 #pragma unroll
-        for (int k = 0; k < 4; ++k) m = fmaxf(m, fabsf(st[a][n][k]));
+        for (int k = 0; k < 4; ++k) m = __builtin_elementwise_maximum(m, fabsf(st[a][n][k]));
       const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
       m = nn_max(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
       const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);

@@ -108,7 +108,7 @@ __device__ __forceinline__ void store_f16l(float* item, int row0, int nt, int g,
 #pragma unroll
   for (int s = 0; s < 2; ++s) {
     const f32x4 v = s ? v1 : v0;
-    float m = fmaxf(fmaxf(fabsf(v[0]), fabsf(v[1])), fmaxf(fabsf(v[2]), fabsf(v[3])));
+    float m = abs_max4(v);
     const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(m), __float_as_uint(m), false, false);
     m = nn_max(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
     const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(m), __float_as_uint(m), false, false);
@@ -513,7 +513,7 @@ void chunk_state_chain_kernel(ChunkStateArgs p, StatePassingArgs sp, ChainPlan p
   auto publish_rowmax = [&](int par) __attribute__((always_inline)) {
 #pragma unroll
     for (int q = 0; q < PTW; ++q) {
-      float m = fmaxf(fmaxf(fabsf(st[q][0]), fabsf(st[q][1])), fmaxf(fabsf(st[q][2]), fabsf(st[q][3])));
+      float m = abs_max4(st[q]);
       // across the lane groups g (lanes i, i + 16, i + 32, i + 48): swap with
       // the neighbouring 16-lane row, then with the other 32-lane half
       {

@@ -113,6 +113,15 @@ __device__ __forceinline__ float nn_max(float a, float b) {
   return __uint_as_float(max(__float_as_uint(a), __float_as_uint(b)));
 }
 
+// Largest magnitude of v's elements (IEEE maximum: v_maximum3_f32 with abs
+// modifiers, two instructions for four values; fmaxf on an MFMA result or an
+// opaque value would quiet each input first, and it drops a NaN that
+// maximum keeps).
+__device__ __forceinline__ float abs_max4(f32x4 v) {
+  return __builtin_elementwise_maximum(__builtin_elementwise_maximum(fabsf(v[0]), fabsf(v[1])),
+                                       __builtin_elementwise_maximum(fabsf(v[2]), fabsf(v[3])));
+}
+
 // SSD_STATE_F16S_LOCAL: the f32 slot, within a [P][N] item, that holds the
 // scale of row p's n tile t (columns 16 t .. 16 t + 15) -- the item's
 // P x N/16 scales, in (p, t) order, packed into the second halves (unused by

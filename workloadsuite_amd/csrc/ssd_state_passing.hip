@@ -276,7 +276,7 @@ __global__ __launch_bounds__(256) void state_passing_f16s_kernel(StatePassingArg
     asm volatile("" : "+v"(val));  // from the f32 state (no fusing of the recurrence into the rounding)
     float m = 0.f;
 #pragma unroll
-    for (int k = 0; k < SPT; ++k) m = fmaxf(m, fabsf(val[k]));
+    for (int k = 0; k < SPT; ++k) m = __builtin_elementwise_maximum(m, fabsf(val[k]));
     m = row_max<TPR>(m);
     const int e = m > 0.f ? min(max(__builtin_amdgcn_frexp_expf(m) - 15, -100), 100) : 0;
     H hv;
