@@ -760,3 +760,55 @@ def test_random_shapes_vs_oracle(k, dtype, Q, N, g, h, b, nc, use_dt, use_init):
     tol = tolerance(dtype)
     assert_close(Y, Yr, tol)
     assert_close(final, fr, tol)
+
+
+def _sweep_cases(n, seed=2024):
+    """Wider seeded random shapes than _random_cases: up to 8 groups and 8
+    heads per group, 96-320 heads at chunk 256 / d_state 128 (the state
+    chain's plans), 1-3 batch rows, 1-6 chunks, the split hand-over and the
+    allocation-free entry point (where its array holds the workspace)."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for k in range(n):
+        dtype = [torch.float32, torch.bfloat16, torch.float16][k % 3]
+        Q = int(rng.choice([64, 128, 256]))
+        N = int(rng.choice([16, 32, 64, 128]))
+        g = int(rng.choice([1, 2, 4, 8]))
+        h = g * int(rng.integers(1, 9))
+        if k % 7 == 3 and dtype != torch.float32:
+            Q, N, h = 256, 128, int(rng.choice([96, 160, 200, 320]))
+        b, nc = int(rng.integers(1, 4)), int(rng.integers(1, 7))
+        if b * h * Q * nc > 400_000:
+            nc = max(1, 400_000 // (b * h * Q))
+        use_dt, use_init = bool(rng.integers(0, 2)), bool(rng.integers(0, 2))
+        split = dtype != torch.float32 and rng.integers(0, 4) == 0
+        noalloc = bool(rng.integers(0, 5) == 0) and b * h * nc * 64 * N * 8 < (128 << 20)
+        cases.append((k, dtype, Q, N, g, h, b, nc, use_dt, use_init, bool(split), noalloc))
+    return cases
+
+
+@pytest.mark.parametrize("k,dtype,Q,N,g,h,b,nc,use_dt,use_init,split,noalloc", _sweep_cases(120))
+def test_random_forward_sweep(k, dtype, Q, N, g, h, b, nc, use_dt, use_init, split, noalloc):
+    """ssd_forward (or ssd_forward_noalloc) on seeded random shapes against
+    the chunked oracle, Y and the final state, with the checks of
+    test_random_shapes_vs_oracle."""
+    say("sweep", k, dtype, Q, N, g, h, b, nc, use_dt, use_init, split, noalloc)
+    cfg = CONFIGS["C2"].scaled(batch=b, seqlen=Q * nc, nheads=h, dstate=N, chunk=Q, ngroups=g, dtype=dtype,
+                               init_state=use_init)
+    inp = make_inputs(cfg, seed=5000 + k)
+    gen = torch.Generator().manual_seed(7000 + k)
+    dt = (torch.rand(b, Q * nc, h, generator=gen) + 0.1) if use_dt else None
+    d = to_dev(inp)
+    fwd = S.ssd_forward_noalloc if noalloc else S.ssd_forward
+    Y, final = fwd(d["X"], d["A"], d["B"], d["C"], Q, dt=None if dt is None else dt.to(DEV),
+                   initial_states=d["init"], return_final_states=True, state_format="split" if split else None)
+    torch.cuda.synchronize()
+    if dtype == torch.float32:
+        Yr, fr, aY, af, _ = f32_reference_bounds(inp["X"], inp["A"], inp["B"], inp["C"], Q, dt=dt, init=inp["init"])
+        check_within(Y, Yr, aY)
+        check_within(final, fr, af, "final")
+        return
+    Yr, fr = O.ssd_chunked(inp["X"], inp["A"], inp["B"], inp["C"], Q, dt=dt, initial_states=inp["init"])
+    tol = tolerance(dtype)
+    assert_close(Y, Yr, tol)
+    assert_close(final, fr, tol)
