@@ -52,11 +52,13 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs p) {
   float xv[ITERS], zr[ITERS];
 
   // every load of the wave's rows first (ITERS 16-byte state loads in flight
-  // per lane instead of one round trip per row), then the updates and stores
+  // per lane instead of one round trip per row), then the updates and stores.
+  // The state streams through once per step: non-temporal loads and stores
+  // (batch 256 at C3's head shape: 251 -> 227 us per step, batch 4 5.9 -> 5.6)
 #pragma unroll
   for (int it = 0; it < ITERS; ++it) {
     const int row = 16 * wave + RPI * it + rsub;
-    st[it] = *reinterpret_cast<const f32x4*>(sg + row * N + n4);
+    st[it] = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(sg + row * N + n4));
     xv[it] = to_f32<T>(xg[row]);
     if (zg) zr[it] = to_f32<T>(zg[row]);
   }
@@ -71,7 +73,7 @@ __global__ __launch_bounds__(256) void decode_step_kernel(DecodeArgs p) {
       ns[k] = da * st[it][k] + u * bv[k];
       part += cv[k] * ns[k];
     }
-    *reinterpret_cast<f32x4*>(sg + row * N + n4) = ns;
+    __builtin_nontemporal_store(ns, reinterpret_cast<f32x4*>(sg + row * N + n4));
 #pragma unroll
     for (int off = LPR / 2; off >= 1; off >>= 1) part += __shfl_xor(part, off, 64);
     if (lane % LPR == 0) {
